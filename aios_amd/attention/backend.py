@@ -1,0 +1,262 @@
+"""MI355X paged attention backend (drop-in for FlashInferAttentionBackend).
+
+Public surface follows python/aios/attention/flashinfer.py:94-394:
+
+* ``prepare_metadata(batch)`` builds cu_seqlens (pinned host int32), the flat
+  page-index list ``indices`` (device int32, identical to the reference's
+  ``torch.cat([page_table[row, :device_len] ...])``) and sets
+  ``batch.attn_metadata``; here it also builds the per-batch plan on the host
+  (the reference plans lazily on the first layer, flashinfer.py:252-289; both
+  happen once per batch and are reused by every layer).
+* ``forward(q, k, v, kv_cache, layer_id, batch)`` appends the new K/V rows
+  (kernel (a)) and then runs prefill (kernel (b)) or decode (kernels (c),
+  (d) and the combine) through the C ABI, returning ``[tokens, Hq*D]``.
+* ``metadata.get_last_indices(bs)`` = ``cu_seqlens_q[1:bs+1] - 1``.
+
+There is one code path for every supported head dim (64, 96, 128), so the
+reference's torch-SDPA fallback for head_dim 96 (flashinfer.py:19-24,
+328-372) has no counterpart here.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import TYPE_CHECKING
+
+import torch
+
+from aios_amd import _lib, paged
+from aios_amd.core import get_global_ctx
+
+from .base import BaseAttentionBackend, BaseAttentionMetadata
+
+if TYPE_CHECKING:
+    from aios_amd.core import Batch
+    from aios_amd.kvcache import MHAKVCache
+
+SUPPORTED_HEAD_DIMS = frozenset({64, 96, 128})
+SUPPORTED_GROUPS = frozenset({1, 2, 3, 4, 6, 8})
+
+
+@dataclass
+class Mi355xAttentionMetadata(BaseAttentionMetadata):
+    cu_seqlens_q_cpu: torch.Tensor
+    cu_seqlens_k_cpu: torch.Tensor
+    cu_seqlens_q_gpu: torch.Tensor
+    cu_seqlens_k_gpu: torch.Tensor
+    indices: torch.Tensor
+    last_page_len_cpu: torch.Tensor
+    num_qo_heads: int
+    num_kv_heads: int
+    head_dim: int
+    page_size: int
+    pos_encoding_mode: str
+    seq_lens_cpu: torch.Tensor
+    dtype: torch.dtype
+    plan: _lib.AttnPlan
+    shared_prefix_len: int
+    host_staging: torch.Tensor
+    initialized: bool = True
+
+    def get_last_indices(self, bs: int) -> torch.Tensor:
+        return self.cu_seqlens_q_gpu[1 : 1 + bs].to(torch.long) - 1
+
+
+class Mi355xAttentionBackend(BaseAttentionBackend):
+    """Paged prefill/decode on hand-written gfx950 HIP kernels."""
+
+    def __init__(
+        self,
+        config,
+        workspace_size: int = 128 * 1024 * 1024,
+        prefix_chunk_len: int = 0,
+        suffix_split_len: int = 0,
+    ) -> None:
+        self.num_heads = config.num_qo_heads
+        self.num_kv_heads = config.num_kv_heads
+        self.head_dim = config.head_dim
+        self.sm_scale = config.head_dim ** -0.5
+        if self.head_dim not in SUPPORTED_HEAD_DIMS:
+            raise ValueError(
+                f"head_dim {self.head_dim} is not supported (built: {sorted(SUPPORTED_HEAD_DIMS)})"
+            )
+        if self.num_heads % self.num_kv_heads:
+            raise ValueError("query head count must be divisible by KV head count")
+        if self.num_heads // self.num_kv_heads not in SUPPORTED_GROUPS:
+            raise ValueError("GQA group size is not supported")
+        self.prefill_kernel_backend = "hip-mfma"
+        self.decode_kernel_backend = "hip-cascade"
+        self.backend_name = "mi355x-paged-prefill-hip-mfma-decode-hip-cascade"
+        self.workspace_size = workspace_size
+        self.prefix_chunk_len = prefix_chunk_len
+        self.suffix_split_len = suffix_split_len
+        self._workspace: torch.Tensor | None = None
+        self._cached_ones_cpu: torch.Tensor = torch.tensor([], dtype=torch.int32)
+
+    # -- helpers ---------------------------------------------------------------
+    def _get_workspace(self, device: torch.device) -> torch.Tensor:
+        if self._workspace is None or self._workspace.numel() != self.workspace_size:
+            self._workspace = torch.empty(self.workspace_size, dtype=torch.uint8, device=device)
+        return self._workspace
+
+    def _get_ones_cpu(self, bs: int) -> torch.Tensor:
+        if bs <= len(self._cached_ones_cpu):
+            return self._cached_ones_cpu[:bs]
+        next_len = 1 << max(bs - 1, 0).bit_length()
+        self._cached_ones_cpu = torch.ones(next_len, dtype=torch.int32, pin_memory=True)
+        return self._cached_ones_cpu[:bs]
+
+    # -- interface -------------------------------------------------------------
+    def prepare_metadata(self, batch: Batch) -> Mi355xAttentionMetadata:
+        ctx = get_global_ctx()
+        page_table = ctx.page_table
+        assert page_table.is_cuda, "the MI355X backend requires a GPU page table"
+        assert page_table.dtype == torch.int32, "page_table must be int32"
+        reqs = batch.reqs
+        bs = len(reqs)
+        seqlens_q = [req.extend_len for req in reqs]
+        seqlens_k = [req.device_len for req in reqs]
+        row_ids = [int(req.table_idx) for req in reqs]
+        if any(r < 0 or r >= page_table.shape[0] for r in row_ids):
+            raise ValueError("request table_idx outside the page table")
+        if seqlens_k and max(seqlens_k) > page_table.shape[1]:
+            raise ValueError("device_len exceeds the page-table row length")
+        device = page_table.device
+
+        # One pinned staging buffer -> one host-to-device copy per batch:
+        # [cu_q (bs+1) | cu_k (bs+1) | row_ids (bs)].
+        host = torch.empty(3 * bs + 2, dtype=torch.int32, pin_memory=True)
+        cu_q = host[: bs + 1]
+        cu_k = host[bs + 1 : 2 * bs + 2]
+        rows = host[2 * bs + 2 :]
+        cu_q[0] = 0
+        cu_k[0] = 0
+        if bs:
+            cu_q[1:] = torch.tensor(seqlens_q, dtype=torch.int32).cumsum_(0)
+            cu_k[1:] = torch.tensor(seqlens_k, dtype=torch.int32).cumsum_(0)
+            rows.copy_(torch.tensor(row_ids, dtype=torch.int32))
+        dev = host.to(device, non_blocking=True)
+        cu_q_gpu = dev[: bs + 1]
+        cu_k_gpu = dev[bs + 1 : 2 * bs + 2]
+        rows_gpu = dev[2 * bs + 2 :]
+        total_kv = int(cu_k[bs]) if bs else 0
+
+        shared = int(getattr(batch, "shared_prefix_len", 0)) if batch.is_decode else 0
+        plan = _lib.AttnPlan()
+        _lib.check(
+            _lib.lib().aios_attn_plan(
+                _lib.PHASE_DECODE if batch.is_decode else _lib.PHASE_PREFILL,
+                cu_q.data_ptr(),
+                cu_k.data_ptr(),
+                bs,
+                self.num_heads,
+                self.num_kv_heads,
+                self.head_dim,
+                1,
+                shared,
+                self.workspace_size,
+                self.prefix_chunk_len,
+                self.suffix_split_len,
+                plan,
+            ),
+            "aios_attn_plan",
+        )
+
+        indices = torch.empty(total_kv, dtype=torch.int32, device=device)
+        if total_kv:
+            stream = torch.cuda.current_stream(device).cuda_stream
+            _lib.check(
+                _lib.lib().aios_build_indices(
+                    page_table.data_ptr(),
+                    page_table.stride(0),
+                    rows_gpu.data_ptr(),
+                    cu_k_gpu.data_ptr(),
+                    bs,
+                    total_kv,
+                    indices.data_ptr(),
+                    stream,
+                ),
+                "aios_build_indices",
+            )
+
+        metadata = Mi355xAttentionMetadata(
+            cu_seqlens_q_cpu=cu_q,
+            cu_seqlens_k_cpu=cu_k,
+            cu_seqlens_q_gpu=cu_q_gpu,
+            cu_seqlens_k_gpu=cu_k_gpu,
+            indices=indices,
+            last_page_len_cpu=self._get_ones_cpu(bs),
+            num_qo_heads=self.num_heads,
+            num_kv_heads=self.num_kv_heads,
+            head_dim=self.head_dim,
+            page_size=1,
+            pos_encoding_mode="NONE",
+            seq_lens_cpu=torch.tensor(seqlens_k, dtype=torch.int32),
+            dtype=ctx.kv_cache.dtype,
+            plan=plan,
+            shared_prefix_len=shared,
+            host_staging=host,
+        )
+        if plan.ws_bytes:
+            self._get_workspace(device)
+        batch.attn_metadata = metadata
+        return metadata
+
+    def forward(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        paged_kv_cache: MHAKVCache,
+        layer_id: int,
+        batch: Batch,
+    ) -> torch.Tensor:
+        if batch.is_prefill:
+            return self._prefill(q, k, v, paged_kv_cache, layer_id, batch)
+        return self._decode(q, k, v, paged_kv_cache, layer_id, batch)
+
+    def _check_q(self, q: torch.Tensor) -> None:
+        if q.ndim != 3 or q.shape[1] != self.num_heads or q.shape[2] != self.head_dim:
+            raise ValueError("q must have shape (tokens, num_qo_heads, head_dim)")
+        if q.dtype != torch.bfloat16:
+            raise ValueError("the MI355X attention kernels compute in bfloat16")
+        if q.stride(2) != 1 or q.stride(1) != self.head_dim:
+            raise ValueError("q must have contiguous (heads, head_dim) rows")
+
+    def _layer_caches(self, paged_kv_cache: MHAKVCache, layer_id: int):
+        k_cache = paged_kv_cache.k_cache(layer_id)
+        v_cache = paged_kv_cache.v_cache(layer_id)
+        if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+            raise ValueError("per-layer KV caches must be contiguous")
+        if k_cache.dtype != torch.bfloat16:
+            raise ValueError("the MI355X attention kernels read a bfloat16 KV cache")
+        return k_cache, v_cache
+
+    def _prefill(self, q, k, v, paged_kv_cache, layer_id, batch) -> torch.Tensor:
+        assert batch.is_prefill, "prefill backend expects a prefill batch"
+        metadata = batch.attn_metadata
+        assert isinstance(metadata, Mi355xAttentionMetadata)
+        self._check_q(q)
+        if q.shape[0] != metadata.plan.total_q:
+            raise RuntimeError("prefill request lengths do not match flat Q tokens")
+        paged_kv_cache.store_kv(k, v, batch.out_loc.view(-1), layer_id)
+        k_cache, v_cache = self._layer_caches(paged_kv_cache, layer_id)
+        out = paged.prefill(metadata.plan, q, k_cache.view(-1, self.num_kv_heads, self.head_dim),
+                            v_cache.view(-1, self.num_kv_heads, self.head_dim), metadata.indices,
+                            metadata.cu_seqlens_q_gpu, metadata.cu_seqlens_k_gpu,
+                            sm_scale=self.sm_scale)
+        return out.reshape(q.size(0), -1)
+
+    def _decode(self, q, k, v, paged_kv_cache, layer_id, batch) -> torch.Tensor:
+        assert batch.is_decode, "decode backend expects a decode batch"
+        bsz = batch.size
+        assert q.size(0) == bsz, "decode batch must contain one flat token per request"
+        metadata = batch.attn_metadata
+        assert isinstance(metadata, Mi355xAttentionMetadata)
+        self._check_q(q)
+        paged_kv_cache.store_kv(k, v, batch.out_loc.view(-1), layer_id)
+        k_cache, v_cache = self._layer_caches(paged_kv_cache, layer_id)
+        ws = self._get_workspace(q.device) if metadata.plan.ws_bytes else None
+        out = paged.decode(metadata.plan, q, k_cache.view(-1, self.num_kv_heads, self.head_dim),
+                           v_cache.view(-1, self.num_kv_heads, self.head_dim), metadata.indices,
+                           metadata.cu_seqlens_k_gpu, workspace=ws, sm_scale=self.sm_scale)
+        return out.reshape(bsz, -1)

@@ -1,0 +1,345 @@
+// C ABI of the attention backend: validation, host-side planning and launch.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/aios_attn.h"
+#include "kernels.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return AIOS_OK;
+  return fail(AIOS_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+}
+
+int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+int32_t cdiv(int32_t a, int32_t b) { return (a + b - 1) / b; }
+
+// Compute units of the current device, looked up once per process (host
+// query only; no device synchronisation).
+int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* aios_last_error(void) { return g_err; }
+
+const char* aios_version(void) { return "aios-mi355x-attn 0.1 gfx950"; }
+
+int aios_kv_append(void* k_cache, void* v_cache, int64_t num_slots, int64_t cache_tok_stride,
+                   const int32_t* out_loc, const void* k, int64_t k_tok_stride, const void* v,
+                   int64_t v_tok_stride, int64_t n_tokens, int64_t width, int32_t elem_bytes,
+                   void* stream) {
+  if (n_tokens < 0 || width <= 0 || num_slots < 0)
+    return fail(AIOS_ERR_INVALID, "kv_append: bad sizes (n_tokens=%lld width=%lld)",
+                (long long)n_tokens, (long long)width);
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8)
+    return fail(AIOS_ERR_UNSUPPORTED, "kv_append: elem_bytes %d", elem_bytes);
+  if (cache_tok_stride < width || k_tok_stride < 0 || v_tok_stride < 0)
+    return fail(AIOS_ERR_INVALID, "kv_append: stride smaller than row width");
+  if (n_tokens == 0) return AIOS_OK;
+  if (!k_cache || !v_cache || !out_loc || !k || !v)
+    return fail(AIOS_ERR_INVALID, "kv_append: null pointer");
+  const hipError_t e = aios::kv_append(
+      k_cache, v_cache, num_slots, cache_tok_stride * elem_bytes, out_loc, k,
+      k_tok_stride * elem_bytes, v, v_tok_stride * elem_bytes, n_tokens, width * elem_bytes,
+      static_cast<hipStream_t>(stream));
+  return check_hip(e, "kv_append launch");
+}
+
+int aios_attn_plan(int32_t phase, const int32_t* cu_q, const int32_t* cu_k, int32_t batch,
+                   int32_t hq, int32_t hkv, int32_t d, int32_t page_size, int32_t shared_prefix,
+                   int64_t ws_bytes, int32_t prefix_chunk_len, int32_t suffix_split_len,
+                   aios_attn_plan_t* p) {
+  if (!p) return fail(AIOS_ERR_INVALID, "plan: null plan");
+  memset(p, 0, sizeof(*p));
+  if (phase != AIOS_PHASE_PREFILL && phase != AIOS_PHASE_DECODE)
+    return fail(AIOS_ERR_INVALID, "plan: unknown phase %d", phase);
+  if (page_size != 1) return fail(AIOS_ERR_UNSUPPORTED, "plan: only page_size=1 is supported");
+  if (batch < 0 || !cu_q || !cu_k) return fail(AIOS_ERR_INVALID, "plan: bad batch arrays");
+  if (hq <= 0 || hkv <= 0 || d <= 0)
+    return fail(AIOS_ERR_INVALID, "plan: head counts and head_dim must be positive");
+  if (hq % hkv) return fail(AIOS_ERR_INVALID, "query head count must be divisible by KV head count");
+  const int32_t G = hq / hkv;
+  if (!aios::tile_supported(d) || !aios::suffix_supported(d, G))
+    return fail(AIOS_ERR_UNSUPPORTED, "plan: head_dim %d with group %d is not built", d, G);
+  if (cu_q[0] != 0 || cu_k[0] != 0) return fail(AIOS_ERR_INVALID, "plan: cu_seqlens must start at 0");
+  int32_t max_q = 0, max_kv = 0, min_kv = 0x7fffffff;
+  for (int32_t b = 0; b < batch; ++b) {
+    const int32_t ql = cu_q[b + 1] - cu_q[b];
+    const int32_t kl = cu_k[b + 1] - cu_k[b];
+    if (ql < 0 || kl < 0) return fail(AIOS_ERR_INVALID, "plan: cu_seqlens must be non-decreasing");
+    if (kl < ql) return fail(AIOS_ERR_INVALID, "cached_len + query length must equal KV length");
+    if (phase == AIOS_PHASE_DECODE && ql != 1)
+      return fail(AIOS_ERR_INVALID, "decode batch must contain one flat token per request");
+    if (ql > max_q) max_q = ql;
+    if (kl > max_kv) max_kv = kl;
+    if (kl < min_kv) min_kv = kl;
+  }
+  if (batch == 0) min_kv = 0;
+  p->phase = phase;
+  p->batch_size = batch;
+  p->num_qo_heads = hq;
+  p->num_kv_heads = hkv;
+  p->head_dim = d;
+  p->group = G;
+  p->total_q = cu_q[batch];
+  p->total_kv = cu_k[batch];
+  p->max_q_len = max_q;
+  p->max_kv_len = max_kv;
+  const int cus = device_cus();
+
+  if (phase == AIOS_PHASE_PREFILL) {
+    // Query rows per workgroup = NW*32 (token, head) pairs.
+    int nw = 4;
+    const int64_t rows_needed = (int64_t)max_q * G;
+    while (nw > 1 && (int64_t)(nw / 2) * 32 >= rows_needed) nw /= 2;
+    // Prefer more, smaller workgroups while the grid is below one per CU.
+    while (nw > 1 && (int64_t)cdiv(max_q, (nw * 32) / G) * hkv * batch < cus / 2) nw /= 2;
+    const int32_t q_tile = (nw * 32) / G;
+    if (q_tile < 1) return fail(AIOS_ERR_UNSUPPORTED, "plan: group %d too large for prefill", G);
+    p->prefill_waves = nw;
+    p->prefill_q_tile = q_tile;
+    p->num_q_tiles = max_q > 0 ? cdiv(max_q, q_tile) : 0;
+    p->ws_bytes = 0;
+    return AIOS_OK;
+  }
+
+  // ---- decode ----------------------------------------------------------------
+  if (shared_prefix < 0 || shared_prefix > min_kv)
+    return fail(AIOS_ERR_INVALID,
+                "plan: shared_prefix_len %d exceeds the shortest row (%d KV positions)",
+                shared_prefix, min_kv);
+  const int32_t m_rows = batch * G;
+  // The MFMA cascade pays off once the group fills at least one 16-row tile.
+  int32_t P = (m_rows >= 16 && batch > 1) ? shared_prefix : 0;
+  int32_t chunk = 0, n_chunks = 0, nw = 0, mgroups = 0;
+  int64_t pre_o = 0, pre_lse = 0, off = 0;
+  if (P > 0) {
+    nw = cdiv(m_rows < 128 ? m_rows : 128, 32);
+    mgroups = cdiv(m_rows, nw * 32);
+    if (prefix_chunk_len > 0) {
+      chunk = (int32_t)align_up(prefix_chunk_len, 32);
+    } else {
+      // About one workgroup per CU, each owning at least one 32-token tile.
+      int32_t want = cdiv(cus, hkv * mgroups);
+      if (want < 1) want = 1;
+      chunk = (int32_t)align_up(cdiv(P, want), 32);
+      if (chunk < 32) chunk = 32;
+    }
+    n_chunks = cdiv(P, chunk);
+    // Shrink the chunk count until the partials fit the workspace.
+    for (;;) {
+      const int64_t o_bytes = (int64_t)n_chunks * hkv * m_rows * d * 4;
+      const int64_t l_bytes = (int64_t)n_chunks * hkv * m_rows * 4;
+      if (align_up(o_bytes, 256) + align_up(l_bytes, 256) <= ws_bytes || n_chunks == 1) break;
+      chunk = (int32_t)align_up((int64_t)chunk * 2, 32);
+      n_chunks = cdiv(P, chunk);
+    }
+    pre_o = 0;
+    pre_lse = align_up((int64_t)n_chunks * hkv * m_rows * d * 4, 256);
+    off = pre_lse + align_up((int64_t)n_chunks * hkv * m_rows * 4, 256);
+  }
+  const int32_t max_suffix = max_kv - P;
+  int32_t split = suffix_split_len > 0 ? suffix_split_len : 0;
+  if (split == 0) {
+    // One split per row unless the rows are long and few.
+    split = max_suffix > 0 ? max_suffix : 1;
+    const int64_t waves = (int64_t)batch * hkv;
+    if (max_suffix > 256 && waves < 2LL * cus) {
+      int32_t want = (int32_t)((2LL * cus + waves - 1) / waves);
+      split = cdiv(max_suffix, want);
+      if (split < 64) split = 64;
+    }
+  }
+  int32_t n_splits = max_suffix > 0 ? cdiv(max_suffix, split) : 1;
+  int64_t suf_o = 0, suf_lse = 0;
+  if (n_splits > 1) {
+    suf_o = off;
+    suf_lse = suf_o + align_up((int64_t)batch * n_splits * hq * d * 4, 256);
+    off = suf_lse + align_up((int64_t)batch * n_splits * hq * 4, 256);
+  }
+  p->prefix_len = P;
+  p->prefix_chunk_len = chunk;
+  p->num_prefix_chunks = n_chunks;
+  p->cascade_rows = m_rows;
+  p->cascade_waves = nw;
+  p->cascade_mgroups = mgroups;
+  p->suffix_split_len = split;
+  p->num_suffix_splits = n_splits;
+  p->ws_prefix_o = pre_o;
+  p->ws_prefix_lse = pre_lse;
+  p->ws_suffix_o = suf_o;
+  p->ws_suffix_lse = suf_lse;
+  p->ws_bytes = off;
+  if (off > ws_bytes)
+    return fail(AIOS_ERR_WORKSPACE, "plan: workspace of %lld bytes is smaller than the %lld needed",
+                (long long)ws_bytes, (long long)off);
+  return AIOS_OK;
+}
+
+static int check_plan(const aios_attn_plan_t* p, int phase) {
+  if (!p) return fail(AIOS_ERR_INVALID, "null plan");
+  if (p->phase != phase)
+    return fail(AIOS_ERR_INVALID, "plan phase %d does not match the call", p->phase);
+  if (!aios::tile_supported(p->head_dim) || !aios::suffix_supported(p->head_dim, p->group))
+    return fail(AIOS_ERR_UNSUPPORTED, "plan: unsupported head_dim/group");
+  return AIOS_OK;
+}
+
+int aios_attn_prefill(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
+                      const void* k_cache, const void* v_cache, int64_t kv_num_pages,
+                      const int32_t* indices,
+                      const int32_t* cu_q, const int32_t* cu_k, void* out, float sm_scale,
+                      void* stream) {
+  int rc = check_plan(p, AIOS_PHASE_PREFILL);
+  if (rc) return rc;
+  if (p->batch_size == 0 || p->total_q == 0) return AIOS_OK;
+  const int D = p->head_dim;
+  if (q_tok_stride < (int64_t)p->num_qo_heads * D || (q_tok_stride % 8) != 0)
+    return fail(AIOS_ERR_INVALID, "prefill: q token stride %lld must be >= Hq*D and a multiple of 8",
+                (long long)q_tok_stride);
+  if (!q || !k_cache || !v_cache || !indices || !cu_q || !cu_k || !out)
+    return fail(AIOS_ERR_INVALID, "prefill: null pointer");
+  if (kv_num_pages < 0) return fail(AIOS_ERR_INVALID, "prefill: negative page count");
+  aios::TileArgs a = {};
+  a.q = static_cast<const aios::bf16*>(q);
+  a.q_tok_stride = q_tok_stride;
+  a.k_cache = static_cast<const aios::bf16*>(k_cache);
+  a.v_cache = static_cast<const aios::bf16*>(v_cache);
+  a.kv_tok_stride = (int64_t)p->num_kv_heads * D;
+  a.num_pages = kv_num_pages;
+  a.indices = indices;
+  a.cu_q = cu_q;
+  a.cu_k = cu_k;
+  a.num_qo_heads = p->num_qo_heads;
+  a.num_kv_heads = p->num_kv_heads;
+  a.group = p->group;
+  a.scale_log2 = sm_scale * aios::kLog2e;
+  a.out = static_cast<aios::bf16*>(out);
+  a.q_tile = p->prefill_q_tile;
+  return check_hip(aios::launch_prefill(D, p->prefill_waves, a, p->num_q_tiles, p->batch_size,
+                                        static_cast<hipStream_t>(stream)),
+                   "prefill launch");
+}
+
+int aios_attn_decode(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
+                     const void* k_cache, const void* v_cache, int64_t kv_num_pages,
+                     const int32_t* indices,
+                     const int32_t* cu_k, void* out, void* workspace, int64_t workspace_bytes,
+                     float sm_scale, void* stream) {
+  int rc = check_plan(p, AIOS_PHASE_DECODE);
+  if (rc) return rc;
+  if (p->batch_size == 0) return AIOS_OK;
+  const int D = p->head_dim;
+  if (q_tok_stride < (int64_t)p->num_qo_heads * D || (q_tok_stride % 8) != 0)
+    return fail(AIOS_ERR_INVALID, "decode: q token stride %lld must be >= Hq*D and a multiple of 8",
+                (long long)q_tok_stride);
+  if (p->ws_bytes > workspace_bytes || (p->ws_bytes > 0 && !workspace))
+    return fail(AIOS_ERR_WORKSPACE, "decode: workspace of %lld bytes is smaller than the %lld needed",
+                (long long)workspace_bytes, (long long)p->ws_bytes);
+  if (((uintptr_t)workspace & 255) != 0)
+    return fail(AIOS_ERR_INVALID, "decode: workspace must be 256-byte aligned");
+  if (!q || !k_cache || !v_cache || !indices || !cu_k || !out)
+    return fail(AIOS_ERR_INVALID, "decode: null pointer");
+  if (kv_num_pages < 0) return fail(AIOS_ERR_INVALID, "decode: negative page count");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const aios::bf16* qp = static_cast<const aios::bf16*>(q);
+  const aios::bf16* kc = static_cast<const aios::bf16*>(k_cache);
+  const aios::bf16* vc = static_cast<const aios::bf16*>(v_cache);
+  const int64_t kv_stride = (int64_t)p->num_kv_heads * D;
+  const float scale_log2 = sm_scale * aios::kLog2e;
+
+  if (p->prefix_len > 0) {
+    aios::TileArgs a = {};
+    a.q = qp;
+    a.q_tok_stride = q_tok_stride;
+    a.k_cache = kc;
+    a.v_cache = vc;
+    a.kv_tok_stride = kv_stride;
+    a.num_pages = kv_num_pages;
+    a.indices = indices;
+    a.num_qo_heads = p->num_qo_heads;
+    a.num_kv_heads = p->num_kv_heads;
+    a.group = p->group;
+    a.scale_log2 = scale_log2;
+    a.prefix_len = p->prefix_len;
+    a.chunk_len = p->prefix_chunk_len;
+    a.m_rows = p->cascade_rows;
+    a.part_o = reinterpret_cast<float*>(ws + p->ws_prefix_o);
+    a.part_lse = reinterpret_cast<float*>(ws + p->ws_prefix_lse);
+    rc = check_hip(aios::launch_cascade(D, p->cascade_waves, a, p->num_prefix_chunks,
+                                        p->cascade_mgroups, s),
+                   "cascade launch");
+    if (rc) return rc;
+  }
+
+  aios::SuffixArgs sa = {};
+  sa.q = qp;
+  sa.q_tok_stride = q_tok_stride;
+  sa.k_cache = kc;
+  sa.v_cache = vc;
+  sa.kv_tok_stride = kv_stride;
+  sa.num_pages = kv_num_pages;
+  sa.indices = indices;
+  sa.cu_k = cu_k;
+  sa.batch = p->batch_size;
+  sa.num_qo_heads = p->num_qo_heads;
+  sa.num_kv_heads = p->num_kv_heads;
+  sa.scale_log2 = scale_log2;
+  sa.prefix_len = p->prefix_len;
+  sa.split_len = p->suffix_split_len;
+  sa.num_splits = p->num_suffix_splits;
+  sa.pre_o = reinterpret_cast<const float*>(ws + p->ws_prefix_o);
+  sa.pre_lse = reinterpret_cast<const float*>(ws + p->ws_prefix_lse);
+  sa.pre_chunks = p->prefix_len > 0 ? p->num_prefix_chunks : 0;
+  sa.m_rows = p->cascade_rows;
+  sa.suf_o = reinterpret_cast<float*>(ws + p->ws_suffix_o);
+  sa.suf_lse = reinterpret_cast<float*>(ws + p->ws_suffix_lse);
+  sa.out = static_cast<aios::bf16*>(out);
+  const bool single = p->num_suffix_splits == 1;
+  rc = check_hip(aios::launch_suffix(D, p->group, single, sa, s), "suffix launch");
+  if (rc || single) return rc;
+  return check_hip(aios::launch_combine(D, p->group, sa, s), "combine launch");
+}
+
+int aios_build_indices(const int32_t* page_table, int64_t page_table_stride,
+                       const int32_t* row_ids, const int32_t* cu_k, int32_t batch,
+                       int32_t total_kv, int32_t* indices_out, void* stream) {
+  if (batch < 0 || total_kv < 0 || page_table_stride <= 0)
+    return fail(AIOS_ERR_INVALID, "build_indices: bad sizes");
+  if (batch == 0 || total_kv == 0) return AIOS_OK;
+  if (!page_table || !row_ids || !cu_k || !indices_out)
+    return fail(AIOS_ERR_INVALID, "build_indices: null pointer");
+  return check_hip(aios::build_indices(page_table, page_table_stride, row_ids, cu_k, batch,
+                                       total_kv, indices_out, static_cast<hipStream_t>(stream)),
+                   "build_indices launch");
+}
+
+}  // extern "C"

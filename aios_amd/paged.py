@@ -1,0 +1,140 @@
+"""Functional wrappers over the C ABI (plan / prefill / decode / kv_append).
+
+These take torch tensors, check the layouts the kernels assume, and pass raw
+device pointers plus the current HIP stream to libaios_attn.so.  The
+reference-shaped backend (``aios_amd.attention``) is built on them.
+"""
+from __future__ import annotations
+
+import torch
+
+from aios_amd import _lib
+
+DEFAULT_WORKSPACE = 128 * 1024 * 1024
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _host_i32(x) -> torch.Tensor:
+    t = torch.as_tensor(x, dtype=torch.int32)
+    if t.device.type != "cpu":
+        raise ValueError("cu_seqlens for planning must be host tensors")
+    return t.contiguous()
+
+
+def plan(phase: str, cu_q, cu_k, num_qo_heads: int, num_kv_heads: int, head_dim: int, *,
+         shared_prefix_len: int = 0, workspace_bytes: int = DEFAULT_WORKSPACE,
+         prefix_chunk_len: int = 0, suffix_split_len: int = 0) -> _lib.AttnPlan:
+    """Host-only schedule for one batch (aios_attn_plan)."""
+    cu_q = _host_i32(cu_q)
+    cu_k = _host_i32(cu_k)
+    if cu_q.numel() != cu_k.numel() or cu_q.numel() < 1:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must have batch_size + 1 entries")
+    p = _lib.AttnPlan()
+    code = _lib.PHASE_DECODE if phase == "decode" else _lib.PHASE_PREFILL
+    _lib.check(
+        _lib.lib().aios_attn_plan(code, cu_q.data_ptr(), cu_k.data_ptr(), cu_q.numel() - 1,
+                                  num_qo_heads, num_kv_heads, head_dim, 1, shared_prefix_len,
+                                  workspace_bytes, prefix_chunk_len, suffix_split_len, p),
+        "aios_attn_plan",
+    )
+    return p
+
+
+def _check_q(q: torch.Tensor, p: _lib.AttnPlan) -> None:
+    if q.dtype != torch.bfloat16 or not q.is_cuda:
+        raise ValueError("q must be a bfloat16 GPU tensor")
+    if q.ndim != 3 or q.shape[1] != p.num_qo_heads or q.shape[2] != p.head_dim:
+        raise ValueError("q must have shape (tokens, num_qo_heads, head_dim)")
+    if q.stride(2) != 1 or q.stride(1) != p.head_dim:
+        raise ValueError("q must have contiguous (heads, head_dim) rows")
+
+
+def _check_cache(c: torch.Tensor, p: _lib.AttnPlan) -> None:
+    if c.dtype != torch.bfloat16 or not c.is_cuda or not c.is_contiguous():
+        raise ValueError("KV cache must be a contiguous bfloat16 GPU tensor")
+    if c.shape[-1] != p.head_dim or c.shape[-2] != p.num_kv_heads:
+        raise ValueError("KV cache must end in (num_kv_heads, head_dim)")
+    if c.numel() != c.shape[0] * p.num_kv_heads * p.head_dim:
+        raise ValueError("KV cache must be (num_pages, [1,] num_kv_heads, head_dim)")
+
+
+def _check_i32(t: torch.Tensor, name: str, n: int) -> None:
+    if t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous() or t.numel() < n:
+        raise ValueError(f"{name} must be a contiguous int32 GPU tensor of >= {n} entries")
+
+
+def decode(p: _lib.AttnPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+           indices: torch.Tensor, cu_k: torch.Tensor, *, out: torch.Tensor | None = None,
+           workspace: torch.Tensor | None = None, sm_scale: float | None = None) -> torch.Tensor:
+    """Paged decode attention of one layer: returns [B, Hq, D] bf16."""
+    if p.phase != _lib.PHASE_DECODE:
+        raise ValueError("plan was not built for decode")
+    _check_q(q, p)
+    if q.shape[0] != p.batch_size:
+        raise ValueError("decode batch must contain one flat token per request")
+    _check_cache(k_cache, p)
+    _check_cache(v_cache, p)
+    _check_i32(indices, "indices", p.total_kv)
+    _check_i32(cu_k, "cu_k", p.batch_size + 1)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if p.ws_bytes and (workspace is None or workspace.numel() < p.ws_bytes):
+        raise RuntimeError(f"decode needs a workspace of {p.ws_bytes} bytes")
+    scale = p.head_dim ** -0.5 if sm_scale is None else sm_scale
+    _lib.check(
+        _lib.lib().aios_attn_decode(
+            p, q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+            k_cache.shape[0], indices.data_ptr(), cu_k.data_ptr(), out.data_ptr(),
+            workspace.data_ptr() if workspace is not None else None,
+            workspace.numel() if workspace is not None else 0, scale, _stream(q.device)),
+        "aios_attn_decode",
+    )
+    return out
+
+
+def prefill(p: _lib.AttnPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+            indices: torch.Tensor, cu_q: torch.Tensor, cu_k: torch.Tensor, *,
+            out: torch.Tensor | None = None, sm_scale: float | None = None) -> torch.Tensor:
+    """Varlen causal paged prefill of one layer: returns [total_q, Hq, D] bf16."""
+    if p.phase != _lib.PHASE_PREFILL:
+        raise ValueError("plan was not built for prefill")
+    _check_q(q, p)
+    if q.shape[0] != p.total_q:
+        raise RuntimeError("prefill request lengths do not match flat Q tokens")
+    _check_cache(k_cache, p)
+    _check_cache(v_cache, p)
+    _check_i32(indices, "indices", p.total_kv)
+    _check_i32(cu_q, "cu_q", p.batch_size + 1)
+    _check_i32(cu_k, "cu_k", p.batch_size + 1)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    scale = p.head_dim ** -0.5 if sm_scale is None else sm_scale
+    _lib.check(
+        _lib.lib().aios_attn_prefill(
+            p, q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+            k_cache.shape[0], indices.data_ptr(), cu_q.data_ptr(), cu_k.data_ptr(), out.data_ptr(),
+            scale,
+            _stream(q.device)),
+        "aios_attn_prefill",
+    )
+    return out
+
+
+def build_indices(page_table: torch.Tensor, row_ids: torch.Tensor, cu_k: torch.Tensor,
+                  total_kv: int) -> torch.Tensor:
+    """Device gather of the flat page-index list (aios_build_indices)."""
+    if page_table.dtype != torch.int32 or page_table.stride(1) != 1:
+        raise ValueError("page_table must be int32 with contiguous rows")
+    _check_i32(row_ids, "row_ids", 0)
+    _check_i32(cu_k, "cu_k", row_ids.numel() + 1)
+    out = torch.empty(total_kv, dtype=torch.int32, device=page_table.device)
+    _lib.check(
+        _lib.lib().aios_build_indices(page_table.data_ptr(), page_table.stride(0),
+                                      row_ids.data_ptr(), cu_k.data_ptr(), row_ids.numel(),
+                                      total_kv, out.data_ptr(), _stream(page_table.device)),
+        "aios_build_indices",
+    )
+    return out

@@ -1,0 +1,174 @@
+/*
+ * aios_attn.h — C ABI of the MI355X (gfx950) paged attention backend for
+ * AIOS-IME.
+ *
+ * Every entry point takes plain device pointers, element strides and a HIP
+ * stream handle (passed as void*), returns an int status (AIOS_OK == 0) and
+ * never synchronises the host.  The library allocates no device memory:
+ * the KV pool, page indices, outputs and the partial-softmax workspace all
+ * belong to the caller.  On a non-zero status, aios_last_error() returns a
+ * thread-local, NUL-terminated message.
+ *
+ * Reference interfaces replaced (paths relative to the 7155/aios tree):
+ *   aios_kv_append     python/aios/kernel/store.py:32-61 (store_cache), the
+ *                      op behind MHAKVCache.store_kv (python/aios/kvcache/
+ *                      mha_pool.py:45-56)
+ *   aios_attn_plan     FlashInferAttentionBackend._initialize_metadata_once
+ *                      -> wrapper.plan(...) (python/aios/attention/
+ *                      flashinfer.py:252-289)
+ *   aios_attn_prefill  BatchPrefillWithPagedKVCacheWrapper.run and the
+ *                      head_dim-96 SDPA fallback (python/aios/attention/
+ *                      flashinfer.py:300-372, 33-91)
+ *   aios_attn_decode   BatchDecodeWithPagedKVCacheWrapper.run (python/aios/
+ *                      attention/flashinfer.py:374-394)
+ *   aios_build_indices the device half of prepare_metadata's
+ *                      torch.cat([page_table[row, :device_len] ...])
+ *                      (python/aios/attention/flashinfer.py:228-230)
+ */
+#ifndef AIOS_ATTN_H
+#define AIOS_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define AIOS_OK 0
+#define AIOS_ERR_INVALID 1     /* bad shape / stride / argument (ValueError)  */
+#define AIOS_ERR_UNSUPPORTED 2 /* head_dim, group size or dtype not built     */
+#define AIOS_ERR_WORKSPACE 3   /* caller workspace smaller than plan needs    */
+#define AIOS_ERR_LAUNCH 4      /* HIP runtime error at launch (RuntimeError)  */
+
+#define AIOS_PHASE_PREFILL 0
+#define AIOS_PHASE_DECODE 1
+
+/* Thread-local message for the last non-zero status of this thread. */
+const char* aios_last_error(void);
+
+/* Version string of the built library. */
+const char* aios_version(void);
+
+/*
+ * Paged KV append (kernel (a)).  For t in [0, n_tokens):
+ *   k_cache[out_loc[t] * cache_tok_stride + 0 .. width) = k[t * k_tok_stride + 0 .. width)
+ *   v_cache[out_loc[t] * cache_tok_stride + 0 .. width) = v[t * v_tok_stride + 0 .. width)
+ * Strides and width are in elements of elem_bytes bytes (2 for bf16/fp16).
+ * k and v have independent token strides (v is usually a strided view into
+ * the fused qkv projection).  out_loc entries outside [0, num_slots) are
+ * skipped (never written).  Replaces kernel/store.py:8-61.
+ */
+int aios_kv_append(void* k_cache, void* v_cache, int64_t num_slots,
+                   int64_t cache_tok_stride, const int32_t* out_loc,
+                   const void* k, int64_t k_tok_stride, const void* v,
+                   int64_t v_tok_stride, int64_t n_tokens, int64_t width,
+                   int32_t elem_bytes, void* stream);
+
+/*
+ * Per-batch schedule, built on the host from host copies of cu_seqlens and
+ * reused by every layer of the batch (the plan-once contract of
+ * flashinfer.py:252-256).  Filled by aios_attn_plan; treat as opaque apart
+ * from ws_bytes (workspace bytes the batch needs).
+ */
+typedef struct aios_attn_plan {
+  int32_t phase;
+  int32_t batch_size;
+  int32_t num_qo_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t group; /* num_qo_heads / num_kv_heads */
+  int32_t total_q;
+  int32_t total_kv;
+  int32_t max_q_len;
+  int32_t max_kv_len;
+  /* decode: shared-prefix cascade */
+  int32_t prefix_len;
+  int32_t prefix_chunk_len;
+  int32_t num_prefix_chunks;
+  int32_t cascade_rows;
+  int32_t cascade_waves;
+  int32_t cascade_mgroups;
+  /* decode: per-row ragged suffix */
+  int32_t suffix_split_len;
+  int32_t num_suffix_splits;
+  /* prefill */
+  int32_t prefill_q_tile;
+  int32_t prefill_waves;
+  int32_t num_q_tiles;
+  int32_t reserved0;
+  /* workspace layout (byte offsets) */
+  int64_t ws_prefix_o;
+  int64_t ws_prefix_lse;
+  int64_t ws_suffix_o;
+  int64_t ws_suffix_lse;
+  int64_t ws_bytes;
+} aios_attn_plan_t;
+
+/*
+ * Build the schedule for one batch.
+ *   cu_q_host, cu_k_host : host int32 arrays of batch_size + 1 prefix sums of
+ *                          per-request query / KV lengths (cu_seqlens_q/k).
+ *   shared_prefix_len    : decode only.  Number of leading KV positions whose
+ *                          page ids are identical in every row (the
+ *                          CandidateGroup shares page_table[:, :P]); 0 = none.
+ *                          Those positions are read once per kv-head.
+ *   prefix_chunk_len, suffix_split_len : tuning overrides (0 = automatic).
+ * Performs validation only on host data; touches no device memory.
+ */
+int aios_attn_plan(int32_t phase, const int32_t* cu_q_host,
+                   const int32_t* cu_k_host, int32_t batch_size,
+                   int32_t num_qo_heads, int32_t num_kv_heads,
+                   int32_t head_dim, int32_t page_size,
+                   int32_t shared_prefix_len, int64_t workspace_bytes,
+                   int32_t prefix_chunk_len, int32_t suffix_split_len,
+                   aios_attn_plan_t* plan_out);
+
+/*
+ * Varlen causal paged prefill (kernel (b)), bf16.  Request r owns query rows
+ * [cu_q[r], cu_q[r+1]) and KV positions [0, kv_len_r) whose pages are
+ * indices[cu_k[r] + pos]; query row i of r sits at absolute position
+ * cached_len_r + i with cached_len_r = kv_len_r - q_len_r and attends to
+ * positions <= cached_len_r + i.  q is [total_q, Hq, D] with token stride
+ * q_tok_stride (elements; head stride D), the per-layer caches are
+ * [kv_num_pages, Hkv, D] contiguous, out is [total_q, Hq, D] contiguous.
+ * cu_q, cu_k and indices are device int32.  A page id outside
+ * [0, kv_num_pages) is read as an all-zero K/V row (never dereferenced).
+ */
+int aios_attn_prefill(const aios_attn_plan_t* plan, const void* q,
+                      int64_t q_tok_stride, const void* k_cache,
+                      const void* v_cache, int64_t kv_num_pages,
+                      const int32_t* indices,
+                      const int32_t* cu_q, const int32_t* cu_k, void* out,
+                      float sm_scale, void* stream);
+
+/*
+ * Paged decode (kernels (c) + (d) + log-sum-exp combine), bf16.  Row b has
+ * one query token q[b] and KV positions [0, kv_len_b) with pages
+ * indices[cu_k[b] + pos].  Positions [0, plan->prefix_len) are read through
+ * row 0's page ids (indices[0 .. prefix_len)) once per kv-head and shared by
+ * all rows; the rest are read per row.  workspace holds the partial softmax
+ * states (plan->ws_bytes bytes).
+ */
+int aios_attn_decode(const aios_attn_plan_t* plan, const void* q,
+                     int64_t q_tok_stride, const void* k_cache,
+                     const void* v_cache, int64_t kv_num_pages,
+                     const int32_t* indices,
+                     const int32_t* cu_k, void* out, void* workspace,
+                     int64_t workspace_bytes, float sm_scale, void* stream);
+
+/*
+ * Gather the flat page-index list of a batch on the device:
+ *   indices_out[cu_k[b] + j] = page_table[row_ids[b] * page_table_stride + j]
+ * for j in [0, cu_k[b+1] - cu_k[b]).  row_ids and cu_k are device int32.
+ */
+int aios_build_indices(const int32_t* page_table, int64_t page_table_stride,
+                       const int32_t* row_ids, const int32_t* cu_k,
+                       int32_t batch_size, int32_t total_kv,
+                       int32_t* indices_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AIOS_ATTN_H */

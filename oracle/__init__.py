@@ -1,0 +1,44 @@
+"""CPU oracle for the AIOS-IME paged attention path — TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, what the reference (7155/aios) computes on
+the attention-backend hot path, so that the gfx950 HIP kernels can be checked
+against it.  It is imported only by ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py``; the product package
+``aios_amd`` never imports it and has no CPU fallback.
+
+Modules and what pins each function (the checks live in tests/test_oracle.py):
+
+  kv_store.py   paged KV scatter (kernel/store.py:8-61)
+                pinned by the reference's scatter known answer
+                (resources/lesson-30-triton-kv-store/run_lesson30.py:7-23) and
+                by brute-force index_put on random inputs.
+  metadata.py   cu_seqlens / flat page indices / last-token rows
+                (attention/flashinfer.py:209-250 in survey numbering)
+                pinned by resources/lesson-26-flashinfer-backend/run_lesson26.py
+                and resources/lesson-32-flashinfer-paged-attention/run_lesson32.py
+                known answers.
+  attention.py  offset-causal GQA paged attention in float64
+                (attention/flashinfer.py:33-91, 328-372, 374-394) pinned by
+                torch's scaled_dot_product_attention (an independent library
+                routine), by the reference's own test case
+                (tests/test_attention_backend.py:25-53: seed 17, cached_len in
+                {0, 2}), and by closed forms (constant keys -> mean of visible
+                values; one visible key -> that value; permutation of pages).
+                The log-sum-exp merge is pinned by the online-softmax known
+                answer (resources/lesson-41-flashattention-online-softmax/
+                run_lesson41.py) and by split-anywhere == unsplit.
+  sdpa_cpu.py   line-for-line torch restatement of the reference's CPU
+                attention path (_sdpa_prefill_attention, flashinfer.py:33-91
+                and the per-request loop :328-372); used as the CPU baseline.
+                Pinned against attention.py.
+  prefix.py     token-LCP prefix-reuse plan (ime.py:1116-1168), pinned by the
+                four cases of resources/lesson-14-prefix-kv-reuse/run_lesson14.py.
+  model.py      float32 CPU restatement of the Qwen3 decoder and the greedy
+                CandidateGroup decode loop (models/qwen3.py:31-173,
+                layers/*.py, ime.py:891-1251) used for full-model Top-1/3
+                parity.  Its building blocks are pinned by closed forms
+                (RMSNorm of a constant row, RoPE at position 0 is identity,
+                RoPE preserves norms); the composition itself is
+                "parity unpinned" against the reference (no reference weights
+                or logits exist offline).
+"""

@@ -1,0 +1,92 @@
+"""The C-ABI library loads and exports every symbol include/aios_attn.h declares.
+
+CPU-only: no kernel is launched; aios_attn_plan is host-only and is
+exercised for its validation and schedule decisions.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from aios_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "aios_attn.h"
+
+
+def _declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(aios_\w+)\s*\(", text, re.M))
+
+
+def test_header_and_binding_agree():
+    assert _declared_functions() == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_symbol():
+    lib = _lib.lib()
+    for name in _lib.EXPORTED_SYMBOLS:
+        assert hasattr(lib, name), name
+    assert lib.aios_version().startswith(b"aios-mi355x")
+
+
+def test_plan_struct_layout_matches_header():
+    # 22 int32 fields followed by 5 int64 fields.
+    assert ctypes.sizeof(_lib.AttnPlan) == 22 * 4 + 5 * 8
+
+
+def _plan(phase, cu_q, cu_k, hq=8, hkv=2, d=96, shared=0, ws=1 << 26, chunk=0, split=0):
+    cu_q = np.asarray(cu_q, dtype=np.int32)
+    cu_k = np.asarray(cu_k, dtype=np.int32)
+    p = _lib.AttnPlan()
+    rc = _lib.lib().aios_attn_plan(phase, cu_q.ctypes.data, cu_k.ctypes.data, len(cu_q) - 1, hq,
+                                   hkv, d, 1, shared, ws, chunk, split, p)
+    return rc, p
+
+
+def test_plan_decode_shared_prefix_schedule():
+    kv = [24 + s for s in (3, 0, 16, 7, 1, 9, 12, 5)]
+    rc, p = _plan(_lib.PHASE_DECODE, np.arange(9), np.cumsum([0] + kv), shared=24)
+    assert rc == 0
+    assert p.prefix_len == 24 and p.cascade_rows == 32 and p.cascade_waves == 1
+    assert p.num_suffix_splits == 1
+    assert p.ws_bytes >= p.num_prefix_chunks * 2 * 32 * 97 * 4
+
+
+def test_plan_rejects_bad_batches():
+    lib = _lib.lib()
+    rc, _ = _plan(_lib.PHASE_DECODE, [0, 2], [0, 5])  # two query tokens in decode
+    assert rc == _lib.AIOS_ERR_INVALID
+    assert b"one flat token" in lib.aios_last_error()
+    rc, _ = _plan(_lib.PHASE_PREFILL, [0, 5], [0, 3])  # kv shorter than q
+    assert rc == _lib.AIOS_ERR_INVALID
+    rc, _ = _plan(_lib.PHASE_DECODE, [0, 1, 2], [0, 10, 20], shared=11)  # prefix too long
+    assert rc == _lib.AIOS_ERR_INVALID
+    rc, _ = _plan(_lib.PHASE_DECODE, [0, 1], [0, 5], hq=6, hkv=4)
+    assert rc == _lib.AIOS_ERR_INVALID
+    assert b"divisible" in lib.aios_last_error()
+    rc, _ = _plan(_lib.PHASE_DECODE, [0, 1], [0, 5], d=80)
+    assert rc == _lib.AIOS_ERR_UNSUPPORTED
+
+
+def test_plan_workspace_too_small():
+    kv = [4096 + 10] * 24
+    rc, p = _plan(_lib.PHASE_DECODE, np.arange(25), np.cumsum([0] + kv), hq=32, hkv=8, d=128,
+                  shared=4096, ws=1024, split=8)
+    assert rc == _lib.AIOS_ERR_WORKSPACE
+
+
+def test_plan_prefill_tiles_cover_queries():
+    rc, p = _plan(_lib.PHASE_PREFILL, [0, 4096], [0, 4096], hq=32, hkv=8, d=128)
+    assert rc == 0
+    assert p.num_q_tiles * p.prefill_q_tile >= 4096
+    assert p.prefill_q_tile * 4 <= p.prefill_waves * 32
+
+
+def test_check_maps_status_to_exceptions():
+    rc, _ = _plan(_lib.PHASE_DECODE, [0, 2], [0, 5])
+    with pytest.raises(ValueError, match="one flat token"):
+        _lib.check(rc, "plan")
