@@ -50,18 +50,16 @@ class AttnPlan(ctypes.Structure):
         ("prefix_chunk_len", ctypes.c_int32),
         ("num_prefix_chunks", ctypes.c_int32),
         ("cascade_rows", ctypes.c_int32),
-        ("cascade_waves", ctypes.c_int32),
         ("cascade_mgroups", ctypes.c_int32),
         ("suffix_split_len", ctypes.c_int32),
         ("num_suffix_splits", ctypes.c_int32),
+        ("suffix_tpg", ctypes.c_int32),
+        ("num_parts", ctypes.c_int32),
         ("prefill_q_tile", ctypes.c_int32),
-        ("prefill_waves", ctypes.c_int32),
         ("num_q_tiles", ctypes.c_int32),
-        ("reserved0", ctypes.c_int32),
-        ("ws_prefix_o", ctypes.c_int64),
-        ("ws_prefix_lse", ctypes.c_int64),
-        ("ws_suffix_o", ctypes.c_int64),
-        ("ws_suffix_lse", ctypes.c_int64),
+        ("stage_mask", ctypes.c_int32),
+        ("ws_parts_o", ctypes.c_int64),
+        ("ws_parts_lse", ctypes.c_int64),
         ("ws_bytes", ctypes.c_int64),
     ]
 

@@ -27,6 +27,11 @@ int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
 int32_t cdiv(int32_t a, int32_t b) { return (a + b - 1) / b; }
 
+// Shared prefixes shorter than this are read per row (no second launch).
+constexpr int32_t kMinCascadePrefix = 128;
+// Partial states per (row, kv-head) the combine merges.
+constexpr int32_t kMaxParts = 64;
+
 // Compute units of the current device, looked up once per process (host
 // query only; no device synchronisation).
 int device_cus() {
@@ -86,7 +91,7 @@ int aios_attn_plan(int32_t phase, const int32_t* cu_q, const int32_t* cu_k, int3
     return fail(AIOS_ERR_INVALID, "plan: head counts and head_dim must be positive");
   if (hq % hkv) return fail(AIOS_ERR_INVALID, "query head count must be divisible by KV head count");
   const int32_t G = hq / hkv;
-  if (!aios::tile_supported(d) || !aios::suffix_supported(d, G))
+  if (!aios::head_dim_supported(d) || !aios::group_supported(G))
     return fail(AIOS_ERR_UNSUPPORTED, "plan: head_dim %d with group %d is not built", d, G);
   if (cu_q[0] != 0 || cu_k[0] != 0) return fail(AIOS_ERR_INVALID, "plan: cu_seqlens must start at 0");
   int32_t max_q = 0, max_kv = 0, min_kv = 0x7fffffff;
@@ -115,18 +120,10 @@ int aios_attn_plan(int32_t phase, const int32_t* cu_q, const int32_t* cu_k, int3
   const int cus = device_cus();
 
   if (phase == AIOS_PHASE_PREFILL) {
-    // Query rows per workgroup = NW*32 (token, head) pairs.
-    int nw = 4;
-    const int64_t rows_needed = (int64_t)max_q * G;
-    while (nw > 1 && (int64_t)(nw / 2) * 32 >= rows_needed) nw /= 2;
-    // Prefer more, smaller workgroups while the grid is below one per CU.
-    while (nw > 1 && (int64_t)cdiv(max_q, (nw * 32) / G) * hkv * batch < cus / 2) nw /= 2;
-    const int32_t q_tile = (nw * 32) / G;
-    if (q_tile < 1) return fail(AIOS_ERR_UNSUPPORTED, "plan: group %d too large for prefill", G);
-    p->prefill_waves = nw;
+    // 128 MFMA rows per workgroup = q_tile tokens x G heads.
+    const int32_t q_tile = 128 / G;
     p->prefill_q_tile = q_tile;
     p->num_q_tiles = max_q > 0 ? cdiv(max_q, q_tile) : 0;
-    p->ws_bytes = 0;
     return AIOS_OK;
   }
 
@@ -136,70 +133,65 @@ int aios_attn_plan(int32_t phase, const int32_t* cu_q, const int32_t* cu_k, int3
                 "plan: shared_prefix_len %d exceeds the shortest row (%d KV positions)",
                 shared_prefix, min_kv);
   const int32_t m_rows = batch * G;
-  // The MFMA cascade pays off once the group fills at least one 16-row tile.
-  int32_t P = (m_rows >= 16 && batch > 1) ? shared_prefix : 0;
-  int32_t chunk = 0, n_chunks = 0, nw = 0, mgroups = 0;
-  int64_t pre_o = 0, pre_lse = 0, off = 0;
-  if (P > 0) {
-    nw = cdiv(m_rows < 128 ? m_rows : 128, 32);
-    mgroups = cdiv(m_rows, nw * 32);
+  // Reading the prefix once per kv-head pays off when the prefix is long
+  // enough to amortise a second launch and the group fills an MFMA tile;
+  // a positive prefix_chunk_len forces it.
+  const bool cascade = shared_prefix > 0 && batch > 1 && m_rows >= 16 &&
+                       (prefix_chunk_len > 0 || shared_prefix >= kMinCascadePrefix);
+  const int32_t P = cascade ? shared_prefix : 0;
+  int32_t chunk = 0, n_chunks = 0, mgroups = 0;
+  if (cascade) {
+    mgroups = cdiv(m_rows, 128);
     if (prefix_chunk_len > 0) {
       chunk = (int32_t)align_up(prefix_chunk_len, 32);
     } else {
-      // About one workgroup per CU, each owning at least one 32-token tile.
+      // About one prefix workgroup per compute unit.
       int32_t want = cdiv(cus, hkv * mgroups);
       if (want < 1) want = 1;
       chunk = (int32_t)align_up(cdiv(P, want), 32);
-      if (chunk < 32) chunk = 32;
     }
     n_chunks = cdiv(P, chunk);
-    // Shrink the chunk count until the partials fit the workspace.
-    for (;;) {
-      const int64_t o_bytes = (int64_t)n_chunks * hkv * m_rows * d * 4;
-      const int64_t l_bytes = (int64_t)n_chunks * hkv * m_rows * 4;
-      if (align_up(o_bytes, 256) + align_up(l_bytes, 256) <= ws_bytes || n_chunks == 1) break;
+  }
+  const int32_t max_suffix = max_kv - P;
+  int32_t tpg = 8;
+  int32_t split;
+  if (suffix_split_len > 0) {
+    split = suffix_split_len;
+  } else if (!cascade && max_suffix <= 64) {
+    tpg = max_suffix > 32 ? 16 : 8;  // one item covers the whole row
+    split = max_suffix > 0 ? max_suffix : 1;
+  } else {
+    split = 4 * tpg;  // one pass per item
+  }
+  int32_t n_splits = max_suffix > 0 ? cdiv(max_suffix, split) : 1;
+  // Bound the parts per (row, kv-head) merged by the combine.
+  while (n_chunks + n_splits > kMaxParts) {
+    if (n_splits > n_chunks) {
+      split *= 2;
+      n_splits = max_suffix > 0 ? cdiv(max_suffix, split) : 1;
+    } else {
       chunk = (int32_t)align_up((int64_t)chunk * 2, 32);
       n_chunks = cdiv(P, chunk);
     }
-    pre_o = 0;
-    pre_lse = align_up((int64_t)n_chunks * hkv * m_rows * d * 4, 256);
-    off = pre_lse + align_up((int64_t)n_chunks * hkv * m_rows * 4, 256);
   }
-  const int32_t max_suffix = max_kv - P;
-  int32_t split = suffix_split_len > 0 ? suffix_split_len : 0;
-  if (split == 0) {
-    // One split per row unless the rows are long and few.
-    split = max_suffix > 0 ? max_suffix : 1;
-    const int64_t waves = (int64_t)batch * hkv;
-    if (max_suffix > 256 && waves < 2LL * cus) {
-      int32_t want = (int32_t)((2LL * cus + waves - 1) / waves);
-      split = cdiv(max_suffix, want);
-      if (split < 64) split = 64;
-    }
-  }
-  int32_t n_splits = max_suffix > 0 ? cdiv(max_suffix, split) : 1;
-  int64_t suf_o = 0, suf_lse = 0;
-  if (n_splits > 1) {
-    suf_o = off;
-    suf_lse = suf_o + align_up((int64_t)batch * n_splits * hq * d * 4, 256);
-    off = suf_lse + align_up((int64_t)batch * n_splits * hq * 4, 256);
-  }
+  const int32_t n_parts = n_chunks + n_splits;
   p->prefix_len = P;
   p->prefix_chunk_len = chunk;
   p->num_prefix_chunks = n_chunks;
   p->cascade_rows = m_rows;
-  p->cascade_waves = nw;
   p->cascade_mgroups = mgroups;
   p->suffix_split_len = split;
   p->num_suffix_splits = n_splits;
-  p->ws_prefix_o = pre_o;
-  p->ws_prefix_lse = pre_lse;
-  p->ws_suffix_o = suf_o;
-  p->ws_suffix_lse = suf_lse;
-  p->ws_bytes = off;
-  if (off > ws_bytes)
+  p->suffix_tpg = tpg;
+  p->num_parts = n_parts;
+  if (n_parts > 1) {
+    p->ws_parts_o = 0;
+    p->ws_parts_lse = align_up((int64_t)batch * hkv * n_parts * G * d * 4, 256);
+    p->ws_bytes = p->ws_parts_lse + align_up((int64_t)batch * hkv * n_parts * G * 4, 256);
+  }
+  if (p->ws_bytes > ws_bytes)
     return fail(AIOS_ERR_WORKSPACE, "plan: workspace of %lld bytes is smaller than the %lld needed",
-                (long long)ws_bytes, (long long)off);
+                (long long)ws_bytes, (long long)p->ws_bytes);
   return AIOS_OK;
 }
 
@@ -207,16 +199,21 @@ static int check_plan(const aios_attn_plan_t* p, int phase) {
   if (!p) return fail(AIOS_ERR_INVALID, "null plan");
   if (p->phase != phase)
     return fail(AIOS_ERR_INVALID, "plan phase %d does not match the call", p->phase);
-  if (!aios::tile_supported(p->head_dim) || !aios::suffix_supported(p->head_dim, p->group))
+  if (!aios::head_dim_supported(p->head_dim) || !aios::group_supported(p->group))
     return fail(AIOS_ERR_UNSUPPORTED, "plan: unsupported head_dim/group");
   return AIOS_OK;
 }
 
+static int check_cache(int64_t kv_num_pages, int64_t tok_stride) {
+  if (kv_num_pages < 0) return fail(AIOS_ERR_INVALID, "negative page count");
+  return AIOS_OK;
+  (void)tok_stride;
+}
+
 int aios_attn_prefill(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
                       const void* k_cache, const void* v_cache, int64_t kv_num_pages,
-                      const int32_t* indices,
-                      const int32_t* cu_q, const int32_t* cu_k, void* out, float sm_scale,
-                      void* stream) {
+                      const int32_t* indices, const int32_t* cu_q, const int32_t* cu_k, void* out,
+                      float sm_scale, void* stream) {
   int rc = check_plan(p, AIOS_PHASE_PREFILL);
   if (rc) return rc;
   if (p->batch_size == 0 || p->total_q == 0) return AIOS_OK;
@@ -226,8 +223,8 @@ int aios_attn_prefill(const aios_attn_plan_t* p, const void* q, int64_t q_tok_st
                 (long long)q_tok_stride);
   if (!q || !k_cache || !v_cache || !indices || !cu_q || !cu_k || !out)
     return fail(AIOS_ERR_INVALID, "prefill: null pointer");
-  if (kv_num_pages < 0) return fail(AIOS_ERR_INVALID, "prefill: negative page count");
-  aios::TileArgs a = {};
+  if ((rc = check_cache(kv_num_pages, (int64_t)p->num_kv_heads * D))) return rc;
+  aios::PrefillArgs a = {};
   a.q = static_cast<const aios::bf16*>(q);
   a.q_tok_stride = q_tok_stride;
   a.k_cache = static_cast<const aios::bf16*>(k_cache);
@@ -241,18 +238,17 @@ int aios_attn_prefill(const aios_attn_plan_t* p, const void* q, int64_t q_tok_st
   a.num_kv_heads = p->num_kv_heads;
   a.group = p->group;
   a.scale_log2 = sm_scale * aios::kLog2e;
-  a.out = static_cast<aios::bf16*>(out);
   a.q_tile = p->prefill_q_tile;
-  return check_hip(aios::launch_prefill(D, p->prefill_waves, a, p->num_q_tiles, p->batch_size,
+  a.out = static_cast<aios::bf16*>(out);
+  return check_hip(aios::launch_prefill(D, 4, a, p->num_q_tiles, p->batch_size,
                                         static_cast<hipStream_t>(stream)),
                    "prefill launch");
 }
 
 int aios_attn_decode(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
                      const void* k_cache, const void* v_cache, int64_t kv_num_pages,
-                     const int32_t* indices,
-                     const int32_t* cu_k, void* out, void* workspace, int64_t workspace_bytes,
-                     float sm_scale, void* stream) {
+                     const int32_t* indices, const int32_t* cu_k, void* out, void* workspace,
+                     int64_t workspace_bytes, float sm_scale, void* stream) {
   int rc = check_plan(p, AIOS_PHASE_DECODE);
   if (rc) return rc;
   if (p->batch_size == 0) return AIOS_OK;
@@ -267,66 +263,47 @@ int aios_attn_decode(const aios_attn_plan_t* p, const void* q, int64_t q_tok_str
     return fail(AIOS_ERR_INVALID, "decode: workspace must be 256-byte aligned");
   if (!q || !k_cache || !v_cache || !indices || !cu_k || !out)
     return fail(AIOS_ERR_INVALID, "decode: null pointer");
-  if (kv_num_pages < 0) return fail(AIOS_ERR_INVALID, "decode: negative page count");
+  if ((rc = check_cache(kv_num_pages, (int64_t)p->num_kv_heads * D))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  const aios::bf16* qp = static_cast<const aios::bf16*>(q);
-  const aios::bf16* kc = static_cast<const aios::bf16*>(k_cache);
-  const aios::bf16* vc = static_cast<const aios::bf16*>(v_cache);
-  const int64_t kv_stride = (int64_t)p->num_kv_heads * D;
-  const float scale_log2 = sm_scale * aios::kLog2e;
+  const int32_t mask = p->stage_mask == 0 ? 3 : p->stage_mask;
 
-  if (p->prefix_len > 0) {
-    aios::TileArgs a = {};
-    a.q = qp;
-    a.q_tok_stride = q_tok_stride;
-    a.k_cache = kc;
-    a.v_cache = vc;
-    a.kv_tok_stride = kv_stride;
-    a.num_pages = kv_num_pages;
-    a.indices = indices;
-    a.num_qo_heads = p->num_qo_heads;
-    a.num_kv_heads = p->num_kv_heads;
-    a.group = p->group;
-    a.scale_log2 = scale_log2;
-    a.prefix_len = p->prefix_len;
-    a.chunk_len = p->prefix_chunk_len;
-    a.m_rows = p->cascade_rows;
-    a.part_o = reinterpret_cast<float*>(ws + p->ws_prefix_o);
-    a.part_lse = reinterpret_cast<float*>(ws + p->ws_prefix_lse);
-    rc = check_hip(aios::launch_cascade(D, p->cascade_waves, a, p->num_prefix_chunks,
-                                        p->cascade_mgroups, s),
-                   "cascade launch");
+  aios::DecodeArgs a = {};
+  a.q = static_cast<const aios::bf16*>(q);
+  a.q_tok_stride = q_tok_stride;
+  a.k_cache = static_cast<const aios::bf16*>(k_cache);
+  a.v_cache = static_cast<const aios::bf16*>(v_cache);
+  a.kv_tok_stride = (int64_t)p->num_kv_heads * D;
+  a.num_pages = kv_num_pages;
+  a.indices = indices;
+  a.cu_k = cu_k;
+  a.batch = p->batch_size;
+  a.num_qo_heads = p->num_qo_heads;
+  a.num_kv_heads = p->num_kv_heads;
+  a.group = p->group;
+  a.scale_log2 = sm_scale * aios::kLog2e;
+  a.prefix_len = p->prefix_len;
+  a.chunk_len = p->prefix_chunk_len;
+  a.n_chunks = p->num_prefix_chunks;
+  a.m_rows = p->cascade_rows;
+  a.m_groups = p->cascade_mgroups > 0 ? p->cascade_mgroups : 1;
+  a.prefix_wgs = p->num_prefix_chunks * p->num_kv_heads * a.m_groups;
+  a.split_len = p->suffix_split_len;
+  a.n_splits = p->num_suffix_splits;
+  a.suffix_items = p->batch_size * p->num_kv_heads * p->num_suffix_splits;
+  a.final_out = p->num_parts == 1 ? 1 : 0;
+  a.parts.o = reinterpret_cast<float*>(ws + p->ws_parts_o);
+  a.parts.lse = reinterpret_cast<float*>(ws + p->ws_parts_lse);
+  a.parts.n_parts = p->num_parts;
+  a.parts.n_chunks = p->num_prefix_chunks;
+  a.out = static_cast<aios::bf16*>(out);
+  if (mask & 1) {
+    rc = check_hip(aios::launch_decode_main(D, p->suffix_tpg, a, s), "decode launch");
     if (rc) return rc;
   }
-
-  aios::SuffixArgs sa = {};
-  sa.q = qp;
-  sa.q_tok_stride = q_tok_stride;
-  sa.k_cache = kc;
-  sa.v_cache = vc;
-  sa.kv_tok_stride = kv_stride;
-  sa.num_pages = kv_num_pages;
-  sa.indices = indices;
-  sa.cu_k = cu_k;
-  sa.batch = p->batch_size;
-  sa.num_qo_heads = p->num_qo_heads;
-  sa.num_kv_heads = p->num_kv_heads;
-  sa.scale_log2 = scale_log2;
-  sa.prefix_len = p->prefix_len;
-  sa.split_len = p->suffix_split_len;
-  sa.num_splits = p->num_suffix_splits;
-  sa.pre_o = reinterpret_cast<const float*>(ws + p->ws_prefix_o);
-  sa.pre_lse = reinterpret_cast<const float*>(ws + p->ws_prefix_lse);
-  sa.pre_chunks = p->prefix_len > 0 ? p->num_prefix_chunks : 0;
-  sa.m_rows = p->cascade_rows;
-  sa.suf_o = reinterpret_cast<float*>(ws + p->ws_suffix_o);
-  sa.suf_lse = reinterpret_cast<float*>(ws + p->ws_suffix_lse);
-  sa.out = static_cast<aios::bf16*>(out);
-  const bool single = p->num_suffix_splits == 1;
-  rc = check_hip(aios::launch_suffix(D, p->group, single, sa, s), "suffix launch");
-  if (rc || single) return rc;
-  return check_hip(aios::launch_combine(D, p->group, sa, s), "combine launch");
+  if (p->num_parts > 1 && (mask & 2))
+    return check_hip(aios::launch_decode_combine(D, a, s), "combine launch");
+  return AIOS_OK;
 }
 
 int aios_build_indices(const int32_t* page_table, int64_t page_table_stride,

@@ -1,0 +1,413 @@
+// Paged decode for a CandidateGroup: shared-prefix cascade (kernel (c)),
+// per-row ragged suffix (kernel (d)) and the log-sum-exp combine.
+//
+// decode_main_kernel is one launch with two kinds of workgroups:
+//   * prefix workgroups (blockIdx.x < prefix_wgs): the MFMA tile engine over
+//     one chunk of the shared prefix for one kv-head and up to 128 of the
+//     batch*G query rows; the prefix KV is therefore read once per kv-head
+//     for the whole group, not once per candidate;
+//   * suffix workgroups: four wavefronts, each owning one (row, kv-head,
+//     split) item of the row's own pages after the prefix.  The 64 lanes form
+//     four 16-lane DPP rows; each DPP row takes every fourth KV position and
+//     each lane holds D/16 dims, so a q.k dot product is a per-lane partial
+//     sum plus a 4-step DPP row reduction.  All page-id loads of the item are
+//     issued together, then all K/V loads, so one item costs two memory
+//     latencies rather than one per position.
+// Every workgroup writes a normalised partial (o, lse) into the parts array
+// (layout in kernels.hpp); decode_combine_kernel merges the parts of each
+// (row, kv-head) with m = max lse_j, w_j = 2^(lse_j - m),
+// out = sum w_j o_j / sum w_j (the split/merge rule of online softmax,
+// resources/lesson-41-flashattention-online-softmax/run_lesson41.py:7-18).
+// When a (row, head) has a single part the suffix wavefront writes bf16
+// output directly and no combine runs.
+#include "engine.hpp"
+
+namespace aios {
+
+template <int E>
+struct Slice {
+  uint32_t w[E / 2];
+};
+
+template <int E>
+__device__ __forceinline__ Slice<E> load_slice(const bf16* p) {
+  Slice<E> r;
+  if constexpr (E == 8) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+    r.w[2] = v.z;
+    r.w[3] = v.w;
+  } else if constexpr (E == 4) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+  } else {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) r.w[i] = q[i];
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// prefix part
+template <int D>
+__device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArgs& a, int wg) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int l16 = lane & 15;
+  const int lg = lane >> 4;
+  const int G = a.group;
+  const int mg = wg % a.m_groups;
+  const int unit = wg / a.m_groups;
+  const int chunk = unit % a.n_chunks;
+  const int h = unit / a.n_chunks;
+
+  TileEngine<D, false> eng;
+  int rows[2];
+  bool ok[2];
+  const bf16* qr[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int m = mg * 128 + wave * 32 + rt * 16 + l16;
+    rows[rt] = m;
+    ok[rt] = m < a.m_rows;
+    const int b = m / G;
+    const int g = m - b * G;
+    qr[rt] = a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + g) * D;
+  }
+  eng.load_q(qr[0], ok[0], qr[1], ok[1]);
+  const int kv_begin = chunk * a.chunk_len;
+  const int kv_end = min(a.prefix_len, kv_begin + a.chunk_len);
+  const int64_t tok_bytes = a.kv_tok_stride * 2;
+  eng.run(lds, reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2,
+          reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2, tok_bytes,
+          a.num_pages, a.indices, kv_begin, kv_end, a.scale_log2);
+
+  constexpr int DT = D / 16;
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const float l_tot = xrow_sum(eng.l_run[rt]);
+    if (!ok[rt]) continue;
+    const int m = rows[rt];
+    const int b = m / G;
+    const int g = m - b * G;
+    const int64_t slot = ((int64_t)b * a.num_kv_heads + h) * a.parts.n_parts + chunk;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    float* po = a.parts.o + (slot * G + g) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<f32x4*>(po + dt * 16 + lg * 4) = eng.o[rt][dt] * inv;
+    if (lg == 0)
+      a.parts.lse[slot * G + g] = l_tot > 0.f ? eng.m_run[rt] + fast_log2(l_tot) : kNegInf;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// suffix part: one wavefront per (row, kv-head, split) item
+template <int D, int G, int TPG>
+__device__ __forceinline__ void decode_suffix_item(const DecodeArgs& a, int item) {
+  constexpr int E = D / 16;
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15;
+  const int lg = lane >> 4;
+  const int split = item % a.n_splits;
+  const int bh = item / a.n_splits;
+  const int h = bh % a.num_kv_heads;
+  const int b = bh / a.num_kv_heads;
+
+  const int base = a.cu_k[b];
+  const int kv_len = a.cu_k[b + 1] - base;
+  const int s_begin = a.prefix_len + split * a.split_len;
+  const int s_end = min(kv_len, s_begin + a.split_len);
+
+  float q[G][E];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const Slice<E> qs =
+        load_slice<E>(a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + g) * D + l16 * E);
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) {
+      q[g][2 * i] = lo_bf16(qs.w[i]);
+      q[g][2 * i + 1] = hi_bf16(qs.w[i]);
+    }
+  }
+
+  float m[G], l[G], acc[G][E];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = kNegInf;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
+  }
+
+  const bf16* kb = a.k_cache + (int64_t)h * D + l16 * E;
+  const bf16* vb = a.v_cache + (int64_t)h * D + l16 * E;
+  for (int t0 = s_begin; t0 < s_end; t0 += 4 * TPG) {
+    int64_t page[TPG];
+#pragma unroll
+    for (int u = 0; u < TPG; ++u) {
+      const int t = t0 + 4 * u + lg;
+      page[u] = t < s_end ? (int64_t)a.indices[base + t] : -1;
+    }
+    Slice<E> ks[TPG], vs[TPG];
+#pragma unroll
+    for (int u = 0; u < TPG; ++u) {
+      if ((uint64_t)page[u] < (uint64_t)a.num_pages) {
+        ks[u] = load_slice<E>(kb + page[u] * a.kv_tok_stride);
+        vs[u] = load_slice<E>(vb + page[u] * a.kv_tok_stride);
+      } else {
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) ks[u].w[i] = vs[u].w[i] = 0u;
+      }
+    }
+    float sc[TPG][G];
+#pragma unroll
+    for (int u = 0; u < TPG; ++u) {
+      const bool ok = t0 + 4 * u + lg < s_end;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) {
+          d = fmaf(q[g][2 * i], lo_bf16(ks[u].w[i]), d);
+          d = fmaf(q[g][2 * i + 1], hi_bf16(ks[u].w[i]), d);
+        }
+        d = row16_sum(d);
+        sc[u][g] = ok ? d * a.scale_log2 : kNegInf;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = sc[0][g];
+#pragma unroll
+      for (int u = 1; u < TPG; ++u) mx = fmaxf(mx, sc[u][g]);
+      const float m_new = fmaxf(m[g], mx);
+      const float mu = (m_new == kNegInf) ? 0.f : m_new;
+      const float alpha = fast_exp2(m[g] - mu);
+      float p[TPG];
+      float ps = 0.f;
+#pragma unroll
+      for (int u = 0; u < TPG; ++u) {
+        p[u] = fast_exp2(sc[u][g] - mu);
+        ps += p[u];
+      }
+      l[g] = l[g] * alpha + ps;
+#pragma unroll
+      for (int i = 0; i < E / 2; ++i) {
+        float a0 = acc[g][2 * i] * alpha;
+        float a1 = acc[g][2 * i + 1] * alpha;
+#pragma unroll
+        for (int u = 0; u < TPG; ++u) {
+          a0 = fmaf(p[u], lo_bf16(vs[u].w[i]), a0);
+          a1 = fmaf(p[u], hi_bf16(vs[u].w[i]), a1);
+        }
+        acc[g][2 * i] = a0;
+        acc[g][2 * i + 1] = a1;
+      }
+      m[g] = m_new;
+    }
+  }
+
+  // Merge the four DPP rows.
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float mx = xrow_max(m[g]);
+    const float mu = (mx == kNegInf) ? 0.f : mx;
+    const float f = fast_exp2(m[g] - mu);
+    l[g] = xrow_sum(l[g] * f);
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[g][e] = xrow_sum(acc[g][e] * f);
+    m[g] = mx;
+  }
+  if (lg != 0) return;
+  if (a.final_out) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
+      uint32_t* pw = reinterpret_cast<uint32_t*>(
+          a.out + ((int64_t)b * a.num_qo_heads + h * G + g) * D + l16 * E);
+#pragma unroll
+      for (int i = 0; i < E / 2; ++i)
+        pw[i] = pack_bf16x2(acc[g][2 * i] * inv, acc[g][2 * i + 1] * inv);
+    }
+  } else {
+    const int64_t slot =
+        ((int64_t)b * a.num_kv_heads + h) * a.parts.n_parts + a.parts.n_chunks + split;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
+      float* po = a.parts.o + (slot * G + g) * D + l16 * E;
+#pragma unroll
+      for (int e = 0; e < E; ++e) po[e] = acc[g][e] * inv;
+      if (l16 == 0) a.parts.lse[slot * G + g] = l[g] > 0.f ? m[g] + fast_log2(l[g]) : kNegInf;
+    }
+  }
+}
+
+template <int D, int G, int TPG>
+__global__ __launch_bounds__(kEngineThreads) void decode_main_kernel(DecodeArgs a) {
+  __shared__ __align__(16) uint8_t lds[KVTile<D>::LDS_BYTES];
+  const int wg = blockIdx.x;
+  if (wg < a.prefix_wgs) {
+    decode_prefix_part<D>(lds, a, wg);
+  } else {
+    const int item = (wg - a.prefix_wgs) * (kEngineThreads / 64) + (threadIdx.x >> 6);
+    if (item < a.suffix_items) decode_suffix_item<D, G, TPG>(a, item);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// combine: one workgroup per (row, kv-head)
+constexpr int kCombineThreads = 256;
+constexpr int kCombineMaxParts = 64;
+constexpr int kCombineBatch = 16;  // parts whose o loads one thread keeps in flight
+
+template <int D, int G>
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeArgs a) {
+  constexpr int E4 = G * D / 4;  // float4 elements per part
+  static_assert(E4 <= kCombineThreads, "one float4 per thread per part");
+  constexpr int R = kCombineThreads / E4;  // threads sharing one element
+  __shared__ float lse_s[kCombineMaxParts * G];
+  __shared__ float mx_s[G];
+  __shared__ float den_s[G];
+  __shared__ f32x4 red[kCombineThreads];
+
+  const int tid = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int b = bh / a.num_kv_heads;
+  const int h = bh - b * a.num_kv_heads;
+  const int np = a.parts.n_parts;
+  const int64_t base = (int64_t)bh * np;
+  const f32x4* po = reinterpret_cast<const f32x4*>(a.parts.o + base * G * D);
+  const float* pl = a.parts.lse + base * G;
+  const int e = tid % E4;
+  const int r = tid / E4;
+  const bool active = r < R;
+  const int g = (e * 4) / D;
+
+  // Issue this thread's o loads first (independent of the weights).
+  f32x4 v[kCombineBatch];
+#pragma unroll
+  for (int k = 0; k < kCombineBatch; ++k) {
+    const int j = r + k * R;
+    v[k] = (active && j < np) ? po[(int64_t)j * E4 + e] : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int i = tid; i < np * G; i += kCombineThreads) lse_s[i] = pl[i];
+  __syncthreads();
+  if (tid < G) {
+    float mx = kNegInf;
+    for (int j = 0; j < np; ++j) mx = fmaxf(mx, lse_s[j * G + tid]);
+    const float mu = (mx == kNegInf) ? 0.f : mx;
+    float den = 0.f;
+    for (int j = 0; j < np; ++j) den += fast_exp2(lse_s[j * G + tid] - mu);
+    mx_s[tid] = mu;
+    den_s[tid] = den;
+  }
+  __syncthreads();
+
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (active) {
+    const float mu = mx_s[g];
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) {
+      const int j = r + k * R;
+      if (j < np) acc += v[k] * fast_exp2(lse_s[j * G + g] - mu);
+    }
+    for (int j0 = r + kCombineBatch * R; j0 < np; j0 += kCombineBatch * R) {
+#pragma unroll
+      for (int k = 0; k < kCombineBatch; ++k) {
+        const int j = j0 + k * R;
+        v[k] = j < np ? po[(int64_t)j * E4 + e] : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int k = 0; k < kCombineBatch; ++k) {
+        const int j = j0 + k * R;
+        if (j < np) acc += v[k] * fast_exp2(lse_s[j * G + g] - mu);
+      }
+    }
+  }
+  if (R > 1) {
+    red[tid] = acc;
+    __syncthreads();
+    if (active && r == 0)
+      for (int rr = 1; rr < R; ++rr) acc += red[rr * E4 + e];
+  }
+  if (active && r == 0) {
+    const float den = den_s[g];
+    const f32x4 res = den > 0.f ? acc * (1.f / den) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const int d = e * 4 - g * D;
+    uint2 packed;
+    packed.x = pack_bf16x2(res[0], res[1]);
+    packed.y = pack_bf16x2(res[2], res[3]);
+    *reinterpret_cast<uint2*>(a.out + ((int64_t)b * a.num_qo_heads + h * G + g) * D + d) = packed;
+  }
+}
+
+bool head_dim_supported(int D) { return D == 64 || D == 96 || D == 128; }
+bool group_supported(int G) {
+  return G == 1 || G == 2 || G == 3 || G == 4 || G == 6 || G == 8;
+}
+
+template <int D, int G>
+static hipError_t launch_main_dg(int tpg, const DecodeArgs& a, hipStream_t s) {
+  const int suffix_wgs = (a.suffix_items + 3) / 4;
+  const dim3 grid(a.prefix_wgs + suffix_wgs);
+  if (grid.x == 0) return hipSuccess;
+  if (tpg == 16)
+    hipLaunchKernelGGL((decode_main_kernel<D, G, 16>), grid, dim3(kEngineThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_main_kernel<D, G, 8>), grid, dim3(kEngineThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_main_d(int tpg, const DecodeArgs& a, hipStream_t s) {
+  switch (a.group) {
+    case 1: return launch_main_dg<D, 1>(tpg, a, s);
+    case 2: return launch_main_dg<D, 2>(tpg, a, s);
+    case 3: return launch_main_dg<D, 3>(tpg, a, s);
+    case 4: return launch_main_dg<D, 4>(tpg, a, s);
+    case 6: return launch_main_dg<D, 6>(tpg, a, s);
+    case 8: return launch_main_dg<D, 8>(tpg, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_decode_main(int D, int tpg, const DecodeArgs& a, hipStream_t s) {
+  switch (D) {
+    case 64: return launch_main_d<64>(tpg, a, s);
+    case 96: return launch_main_d<96>(tpg, a, s);
+    case 128: return launch_main_d<128>(tpg, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int D>
+static hipError_t launch_combine_d(const DecodeArgs& a, hipStream_t s) {
+  const dim3 grid(a.batch * a.num_kv_heads);
+  if (grid.x == 0) return hipSuccess;
+  switch (a.group) {
+    case 1: hipLaunchKernelGGL((decode_combine_kernel<D, 1>), grid, dim3(kCombineThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((decode_combine_kernel<D, 2>), grid, dim3(kCombineThreads), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((decode_combine_kernel<D, 3>), grid, dim3(kCombineThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((decode_combine_kernel<D, 4>), grid, dim3(kCombineThreads), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((decode_combine_kernel<D, 6>), grid, dim3(kCombineThreads), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((decode_combine_kernel<D, 8>), grid, dim3(kCombineThreads), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_combine(int D, const DecodeArgs& a, hipStream_t s) {
+  switch (D) {
+    case 64: return launch_combine_d<64>(a, s);
+    case 96: return launch_combine_d<96>(a, s);
+    case 128: return launch_combine_d<128>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace aios

@@ -1,0 +1,85 @@
+// Varlen causal paged prefill (kernel (b)), also used for cross-keystroke
+// LCP extension (a few new tokens against a cached prefix).
+//
+// One workgroup owns (request r, kv-head h, query tile): q_tile consecutive
+// query tokens times the G query heads of h, packed into the 128 MFMA rows
+// (row = token * G + head), and streams KV positions [0, cached_len +
+// last token of the tile] of r through the tile engine with the offset
+// causal mask key_pos <= cached_len + i (python/aios/attention/
+// flashinfer.py:67-80).  Tiles entirely below the diagonal are unmasked; the
+// mask only bites in the last sub-tiles.
+#include "engine.hpp"
+
+namespace aios {
+
+template <int D>
+__global__ __launch_bounds__(kEngineThreads) void prefill_kernel(PrefillArgs a) {
+  __shared__ __align__(16) uint8_t lds[KVTile<D>::LDS_BYTES];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int l16 = lane & 15;
+  const int lg = lane >> 4;
+  const int G = a.group;
+  const int qt = blockIdx.x;
+  const int h = blockIdx.y;
+  const int r = blockIdx.z;
+  const int q_start = a.cu_q[r];
+  const int q_len = a.cu_q[r + 1] - q_start;
+  if (qt * a.q_tile >= q_len) return;
+  const int kv_base = a.cu_k[r];
+  const int kv_len = a.cu_k[r + 1] - kv_base;
+  const int cached = kv_len - q_len;
+  const int q_hi = min(q_len, (qt + 1) * a.q_tile);
+
+  TileEngine<D, true> eng;
+  bool ok[2];
+  int64_t out_off[2];
+  const bf16* qr[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int m = wave * 32 + rt * 16 + l16;
+    const int i = qt * a.q_tile + m / G;
+    const int g = m - (m / G) * G;
+    ok[rt] = (m < a.q_tile * G) && (i < q_len);
+    qr[rt] = a.q + (int64_t)(q_start + i) * a.q_tok_stride + (int64_t)(h * G + g) * D;
+    out_off[rt] = ((int64_t)(q_start + i) * a.num_qo_heads + (h * G + g)) * D;
+    eng.limit[rt] = cached + i;
+  }
+  eng.load_q(qr[0], ok[0], qr[1], ok[1]);
+  eng.run(lds, reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2,
+          reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2, a.kv_tok_stride * 2,
+          a.num_pages, a.indices + kv_base, 0, min(kv_len, cached + q_hi), a.scale_log2);
+
+  constexpr int DT = D / 16;
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const float l_tot = xrow_sum(eng.l_run[rt]);
+    if (!ok[rt]) continue;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    bf16* po = a.out + out_off[rt];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const f32x4 v = eng.o[rt][dt] * inv;
+      uint2 packed;
+      packed.x = pack_bf16x2(v[0], v[1]);
+      packed.y = pack_bf16x2(v[2], v[3]);
+      *reinterpret_cast<uint2*>(po + dt * 16 + lg * 4) = packed;
+    }
+  }
+}
+
+hipError_t launch_prefill(int D, int NW, const PrefillArgs& a, int q_tiles, int batch,
+                          hipStream_t s) {
+  (void)NW;
+  const dim3 grid(q_tiles, a.num_kv_heads, batch);
+  if (q_tiles == 0 || batch == 0) return hipSuccess;
+  switch (D) {
+    case 64: hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(kEngineThreads), 0, s, a); break;
+    case 96: hipLaunchKernelGGL(prefill_kernel<96>, grid, dim3(kEngineThreads), 0, s, a); break;
+    case 128: hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kEngineThreads), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace aios

@@ -1,0 +1,263 @@
+// MFMA attention tile engine for gfx950, shared by the shared-prefix cascade
+// decode (kernel (c)) and the varlen causal prefill (kernel (b)).
+//
+// A 256-thread workgroup (4 wavefronts) owns one kv-head, one KV position
+// range and up to 128 query rows (each wavefront 32 rows: two 16-row MFMA
+// tiles).  A query row is any (token or candidate, q-head) pair of the GQA
+// group, so all query heads sharing a kv-head share one K/V stream.
+//
+// Data movement: the range's page ids are staged in LDS, then K/V rows are
+// gathered page by page straight from HBM into an LDS ring of four 32-token
+// sub-tiles with global_load_lds_dwordx4 (no VGPR staging), three sub-tiles
+// ahead of the one being consumed.  Rows are stored token-major with the
+// sixteen-byte chunks of each row rotated (K by the token index, V by twice
+// the token index) so that both MFMA operand reads below are bank-conflict
+// free.  Masked or out-of-range positions load a zero row.
+//
+// Math per 32-token sub-tile and wavefront:
+//   S^T = K Q^T         v_mfma_f32_16x16x32_bf16, A = K rows (ds_read_b128),
+//                       B = Q fragments kept in registers
+//   online softmax      one query row per lane column; row max over the four
+//                       lane groups by cross-row shuffles; log2 domain
+//   O^T += V^T P^T      A = V^T read with ds_read_b64_tr_b16 (the LDS
+//                       transpose read) from the token-major V rows, B = P^T,
+//                       which is exactly the fragment each lane holds after
+//                       the S^T step (tokens {4g..4g+3} and {16+4g..16+4g+3}
+//                       of lane group g)
+// This is the offset-causal GQA softmax attention of
+// python/aios/attention/flashinfer.py:33-91 (decode: q_len 1).
+#pragma once
+
+#include "kernels.hpp"
+
+#define AIOS_LDS __attribute__((address_space(3)))
+
+namespace aios {
+
+constexpr int kSubTok = 32;       // KV positions per sub-tile
+constexpr int kRing = 4;          // sub-tiles in the LDS ring
+constexpr int kIdWindow = 1024;   // page ids staged in LDS at a time
+constexpr int kEngineThreads = 256;
+
+// Source of every masked / out-of-range K or V chunk.
+static __device__ __align__(16) uint8_t g_zero_kv_row[512] = {0};
+
+// s_waitcnt with vmcnt <= N and the other counters unconstrained.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Every LDS access this thread issued has completed; then a workgroup
+// barrier.  Plain s_barrier (no fence): the asynchronous LDS loads are
+// waited for explicitly with wait_vmcnt.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
+
+template <int D>
+struct KVTile {
+  static constexpr int ROWB = 2 * D;                 // bytes of one K or V row
+  static constexpr int CPR = D / 8;                  // 16-byte chunks per row
+  static constexpr int SUB_KB = kSubTok * ROWB;      // K bytes per sub-tile
+  static constexpr int SUB_BYTES = 2 * SUB_KB;       // K then V
+  static constexpr int LPS = SUB_BYTES / (kEngineThreads * 16);  // loads / thread / sub-tile
+  static constexpr int RING_BYTES = kRing * SUB_BYTES;
+  static constexpr int LDS_BYTES = RING_BYTES + kIdWindow * 4;
+  static_assert(SUB_BYTES % (kEngineThreads * 16) == 0, "sub-tile must split evenly");
+  static_assert(4 * CPR >= kSubTok && 8 * CPR >= 2 * kSubTok, "rotation range");
+
+  // Chunk slot of (token t, chunk c) and its inverse.
+  static __device__ __forceinline__ int k_slot(int t, int c) { return (c + t) % CPR; }
+  static __device__ __forceinline__ int v_slot(int t, int c) { return (c + 2 * t) % CPR; }
+  static __device__ __forceinline__ int k_chunk(int t, int slot) { return (slot + 4 * CPR - t) % CPR; }
+  static __device__ __forceinline__ int v_chunk(int t, int slot) {
+    return (slot + 8 * CPR - 2 * t) % CPR;
+  }
+};
+
+template <int D, bool CAUSAL>
+struct TileEngine {
+  using T = KVTile<D>;
+  static constexpr int KSTEPS = D / 32;
+  static constexpr int DTILES = D / 16;
+
+  bf16x8 qf[2][KSTEPS];
+  f32x4 o[2][DTILES];
+  float m_run[2];
+  float l_run[2];
+  int limit[2];  // CAUSAL: last visible KV position of the lane's rows
+
+  // Q fragment (B operand of S^T = K Q^T) of the lane's two rows.
+  __device__ __forceinline__ void load_q(const bf16* q0, bool ok0, const bf16* q1, bool ok1) {
+    const int lg = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      qf[0][s] = ok0 ? *reinterpret_cast<const bf16x8*>(q0 + s * 32 + lg * 8) : bf16x8{};
+      qf[1][s] = ok1 ? *reinterpret_cast<const bf16x8*>(q1 + s * 32 + lg * 8) : bf16x8{};
+    }
+  }
+
+  // Stream KV positions [kv_begin, kv_end) of one kv-head (kc / vc point at
+  // head h of page 0; tok_bytes = page stride) whose page ids are
+  // idx[kv_begin .. kv_end).  Leaves o (unnormalised), m_run and the
+  // lane-partial l_run.
+  __device__ void run(uint8_t* lds, const uint8_t* kc, const uint8_t* vc, int64_t tok_bytes,
+                      int64_t num_pages, const int32_t* idx, int kv_begin, int kv_end,
+                      float scale_log2) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l16 = lane & 15;
+    const int lg = lane >> 4;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_run[rt] = kNegInf;
+      l_run[rt] = 0.f;
+    }
+    const int n_sub = (kv_end - kv_begin + kSubTok - 1) / kSubTok;
+    if (n_sub <= 0) return;
+
+    int32_t* ids = reinterpret_cast<int32_t*>(lds + T::RING_BYTES);
+    int win = kv_begin;
+    auto stage_ids = [&]() {
+      for (int i = tid; i < kIdWindow; i += kEngineThreads) {
+        const int p = win + i;
+        ids[i] = p < kv_end ? idx[p] : -1;
+      }
+    };
+    stage_ids();
+    lds_barrier();
+
+    auto issue = [&](int s) {
+      uint8_t* buf = lds + (s & (kRing - 1)) * T::SUB_BYTES;
+      const int pos0 = kv_begin + s * kSubTok;
+#pragma unroll
+      for (int j = 0; j < T::LPS; ++j) {
+        const int off = (j * kEngineThreads + tid) * 16;
+        const bool isv = off >= T::SUB_KB;
+        const int o2 = isv ? off - T::SUB_KB : off;
+        const int t = o2 / T::ROWB;
+        const int slot = (o2 - t * T::ROWB) >> 4;
+        const int c = isv ? T::v_chunk(t, slot) : T::k_chunk(t, slot);
+        const int gp = pos0 + t;
+        const int64_t page = gp < kv_end ? (int64_t)ids[gp - win] : -1;
+        const uint8_t* src = ((uint64_t)page < (uint64_t)num_pages)
+                                 ? (isv ? vc : kc) + page * tok_bytes + c * 16
+                                 : g_zero_kv_row + c * 16;
+        __builtin_amdgcn_global_load_lds(
+            src, (AIOS_LDS void*)(buf + (j * kEngineThreads + wave * 64) * 16), 16, 0, 0);
+      }
+    };
+
+#pragma unroll
+    for (int s = 0; s < kRing - 1; ++s)
+      if (s < n_sub) issue(s);
+
+    for (int it = 0; it < n_sub; ++it) {
+      const int pend = min(kRing - 2, n_sub - 1 - it);
+      if (pend >= 2)
+        wait_vmcnt<2 * T::LPS>();
+      else if (pend == 1)
+        wait_vmcnt<T::LPS>();
+      else
+        wait_vmcnt<0>();
+      lds_barrier();  // sub-tile `it` is in LDS; every wave is done with it-1
+      const int s_next = it + kRing - 1;
+      if (s_next < n_sub) {
+        if (kv_begin + s_next * kSubTok >= win + kIdWindow) {
+          win += kIdWindow;
+          stage_ids();
+          lds_barrier();
+        }
+        issue(s_next);
+      }
+      compute(lds + (it & (kRing - 1)) * T::SUB_BYTES, kv_begin + it * kSubTok, kv_end,
+              scale_log2, l16, lg);
+    }
+  }
+
+  __device__ __forceinline__ void compute(const uint8_t* kb, int kv0, int kv_end, float scale_log2,
+                                          int l16, int lg) {
+    const uint8_t* vb = kb + T::SUB_KB;
+    // S^T tiles: st[rt][tt][i] = S[row rt*16 + l16][token tt*16 + lg*4 + i]
+    f32x4 st[2][2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      st[0][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      st[1][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int t = tt * 16 + l16;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kb + t * T::ROWB +
+                                                           T::k_slot(t, s * 4 + lg) * 16);
+        st[0][tt] = mfma16x16x32(kf, qf[0][s], st[0][tt]);
+        st[1][tt] = mfma16x16x32(kf, qf[1][s], st[1][tt]);
+      }
+    }
+
+    bf16x8 pb[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float x[8];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int pos = kv0 + tt * 16 + lg * 4 + i;
+          bool ok = pos < kv_end;
+          if (CAUSAL) ok = ok && pos <= limit[rt];
+          x[tt * 4 + i] = ok ? st[rt][tt][i] * scale_log2 : kNegInf;
+        }
+      float mx = x[0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) mx = fmaxf(mx, x[j]);
+      mx = xrow_max(mx);
+      const float m_new = fmaxf(m_run[rt], mx);
+      const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run[rt] - m_use);
+      float p[8];
+      float psum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        p[j] = fast_exp2(x[j] - m_use);
+        psum += p[j];
+      }
+      l_run[rt] = l_run[rt] * alpha + psum;
+      m_run[rt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] *= alpha;
+      pb[rt] = __builtin_bit_cast(
+          bf16x8, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                             pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])));
+    }
+
+    // O^T += V^T P^T.  Lane (lg, l16) supplies V[token][dt*16 + 4*(l16%4)..+3]
+    // of tokens lg*4 + l16/4 (first read) and 16 + lg*4 + l16/4 (second read)
+    // and receives V[tokens][dt*16 + l16], the A fragment rows of the MFMA.
+    const int r = l16 >> 2;
+    const int q4 = l16 & 3;
+    const int t0 = lg * 4 + r;
+    const int t1 = 16 + lg * 4 + r;
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int dt = 0; dt < DTILES; ++dt) {
+      const int dim = dt * 16 + 4 * q4;
+      const int c = dim >> 3;
+      const int boff = (dim & 7) * 2;
+      const uint8_t* p0 = vb + t0 * T::ROWB + T::v_slot(t0, c) * 16 + boff;
+      const uint8_t* p1 = vb + t1 * T::ROWB + T::v_slot(t1, c) * 16 + boff;
+      const bf16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((AIOS_LDS bf16x4*)(p0));
+      const bf16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((AIOS_LDS bf16x4*)(p1));
+      const bf16x8 vf = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+      o[0][dt] = mfma16x16x32(vf, pb[0], o[0][dt]);
+      o[1][dt] = mfma16x16x32(vf, pb[1], o[1][dt]);
+    }
+  }
+};
+
+}  // namespace aios

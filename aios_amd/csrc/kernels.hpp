@@ -6,7 +6,19 @@
 
 namespace aios {
 
-struct TileArgs {
+// Partial softmax states of a decode batch live in one workspace array,
+// contiguous per (row b, kv-head h):
+//   parts_o  [B][Hkv][n_parts][G][D] fp32 (normalised o = acc / l)
+//   parts_lse[B][Hkv][n_parts][G]    fp32 (log2-domain m + log2 l; -inf = empty)
+// Slot j < n_chunks holds prefix chunk j; slot n_chunks + s holds suffix split s.
+struct PartsArgs {
+  float* o;
+  float* lse;
+  int32_t n_parts;
+  int32_t n_chunks;
+};
+
+struct DecodeArgs {
   const bf16* q;
   int64_t q_tok_stride;  // elements
   const bf16* k_cache;
@@ -14,24 +26,29 @@ struct TileArgs {
   int64_t kv_tok_stride;  // elements (= Hkv * D)
   int64_t num_pages;      // rows of the per-layer caches; other page ids read as zeros
   const int32_t* indices;
-  const int32_t* cu_q;
   const int32_t* cu_k;
+  int32_t batch;
   int32_t num_qo_heads;
   int32_t num_kv_heads;
   int32_t group;
   float scale_log2;
-  // cascade
+  // shared prefix (cascade) work: chunks x kv-heads x row groups
   int32_t prefix_len;
   int32_t chunk_len;
-  int32_t m_rows;   // batch * group
-  float* part_o;    // [chunks][Hkv][m_rows][D]
-  float* part_lse;  // [chunks][Hkv][m_rows]
-  // prefill
-  bf16* out;
-  int32_t q_tile;  // query tokens per workgroup
+  int32_t n_chunks;
+  int32_t m_rows;      // batch * group
+  int32_t m_groups;
+  int32_t prefix_wgs;  // n_chunks * Hkv * m_groups
+  // per-row suffix work: (row, kv-head, split) items, one wavefront each
+  int32_t split_len;
+  int32_t n_splits;
+  int32_t suffix_items;  // batch * Hkv * n_splits
+  int32_t final_out;     // 1: a single part per (row, head): write bf16 out directly
+  PartsArgs parts;
+  bf16* out;  // [B][Hq][D]
 };
 
-struct SuffixArgs {
+struct PrefillArgs {
   const bf16* q;
   int64_t q_tok_stride;
   const bf16* k_cache;
@@ -39,23 +56,14 @@ struct SuffixArgs {
   int64_t kv_tok_stride;
   int64_t num_pages;
   const int32_t* indices;
+  const int32_t* cu_q;
   const int32_t* cu_k;
-  int32_t batch;
   int32_t num_qo_heads;
   int32_t num_kv_heads;
+  int32_t group;
   float scale_log2;
-  int32_t prefix_len;
-  int32_t split_len;
-  int32_t num_splits;
-  // prefix partials (read when finalising)
-  const float* pre_o;
-  const float* pre_lse;
-  int32_t pre_chunks;
-  int32_t m_rows;
-  // suffix partials (written when num_splits > 1)
-  float* suf_o;    // [batch][num_splits][Hq][D]
-  float* suf_lse;  // [batch][num_splits][Hq]
-  bf16* out;       // [batch][Hq][D]
+  int32_t q_tile;  // query tokens per workgroup
+  bf16* out;
 };
 
 hipError_t kv_append(void* k_cache, void* v_cache, int64_t num_slots, int64_t cache_stride_b,
@@ -67,19 +75,17 @@ hipError_t build_indices(const int32_t* page_table, int64_t pt_stride, const int
                          const int32_t* cu_k, int32_t batch, int32_t max_len,
                          int32_t* indices, hipStream_t stream);
 
-hipError_t launch_cascade(int D, int NW, const TileArgs& a, int chunks, int mgroups,
+// One launch: prefix-chunk workgroups (MFMA tile engine) followed by suffix
+// workgroups (four (row, head, split) items per workgroup).
+hipError_t launch_decode_main(int D, int tpg, const DecodeArgs& a, hipStream_t stream);
+
+// Log-sum-exp merge of every part of each (row, kv-head) into bf16 out.
+hipError_t launch_decode_combine(int D, const DecodeArgs& a, hipStream_t stream);
+
+hipError_t launch_prefill(int D, int NW, const PrefillArgs& a, int q_tiles, int batch,
                           hipStream_t stream);
 
-hipError_t launch_prefill(int D, int NW, const TileArgs& a, int q_tiles, int batch,
-                          hipStream_t stream);
-
-// finalize: merge prefix partials and write bf16 output (num_splits == 1);
-// otherwise write suffix partials for launch_combine.
-hipError_t launch_suffix(int D, int G, bool finalize, const SuffixArgs& a, hipStream_t stream);
-
-hipError_t launch_combine(int D, int G, const SuffixArgs& a, hipStream_t stream);
-
-bool tile_supported(int D);
-bool suffix_supported(int D, int G);
+bool head_dim_supported(int D);
+bool group_supported(int G);
 
 }  // namespace aios

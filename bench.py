@@ -1,0 +1,240 @@
+"""Benchmark: shared-prefix paged decode step on one MI355X.
+
+Workload (default ``long_context``): the Qwen3-4B-shaped long-context stress —
+36 layers, 32 query / 8 KV heads, head_dim 128, bf16, a 4096-token shared
+prefix, 24 candidate rows with previous suffixes drawn U{0..64}, pages
+scattered over a 65,536-page pool.  One step is one decode step of the
+attention path over all 36 layers: per layer, append the 24 new K/V rows
+(kernel (a)), then the shared-prefix cascade (kernel (c)) and the per-row
+suffix + log-sum-exp combine (kernel (d)).  Inputs are resident in HBM before
+the timed region; the per-batch plan is built once before it (it is host-only
+work done once per batch by prepare_metadata).
+
+Prints one JSON line: value = decode-step microseconds (lower is better),
+with the cascade kernel's roofline measured live with HIP events, and the
+reference's CPU attention path (restated, oracle/sdpa_cpu.py) timed on a
+bounded sample on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _traffic(kernel: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (profiles/traffic.json), or None."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        data = json.loads(path.read_text())
+        return data.get(kernel, {}).get("bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def cpu_baseline(wl, max_seconds: float) -> dict:
+    """Reference CPU attention path (restated) on a bounded sample of the step.
+
+    Sample: the 24 rows of ONE layer (gather pages, repeat GQA heads, SDPA per
+    row; flashinfer.py:33-91 / :328-372), timed in bf16 (the reference's
+    dtype), scaled by 36 to microseconds per decode step.
+    """
+    import torch
+
+    from oracle.sdpa_cpu import paged_attention_cpu
+
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    torch.set_num_threads(threads)
+    shape = wl.shape
+    q = wl.q[0].cpu()
+    kc = wl.k_cache[0].cpu()
+    vc = wl.v_cache[0].cpu()
+    idx = wl.indices
+    cu_q = list(range(shape.num_rows + 1))
+    cu_k = wl.cu_k.tolist()
+    scale = shape.head_dim ** -0.5
+    times = []
+    t_start = time.perf_counter()
+    for it in range(3 + 20):
+        t0 = time.perf_counter()
+        paged_attention_cpu(q, kc, vc, idx, cu_q, cu_k, scale)
+        dt = time.perf_counter() - t0
+        if it >= 3:
+            times.append(dt)
+        if time.perf_counter() - t_start > max_seconds and len(times) >= 3:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": med * shape.num_layers * 1e6,
+        "unit": "us/step",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"1 of {shape.num_layers} layers x {shape.num_rows} rows, bf16 torch CPU SDPA per row "
+                   f"(oracle/sdpa_cpu.py), median of {len(times)} after 3 warmups, x{shape.num_layers}; "
+                   f"cpu={_cpu_model()}, os.cpu_count={os.cpu_count()}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--seed", type=int, default=20260814)
+    ap.add_argument("--workload", default="long_context", choices=["long_context", "op_test"])
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--chunk", type=int, default=0, help="prefix chunk override (tuning)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs the "
+              "attention path on a single MI355X and does not shard across GPUs.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from aios_amd import paged
+    from aios_amd.kernel import store_cache
+    from aios_amd.workloads import SHAPES, decode_bytes_per_layer, kv_append_bytes, make_decode_workload
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    shape = SHAPES[args.workload]
+    wl = make_decode_workload(shape, seed=args.seed, device=dev, extra_token=True)
+    n, nl = shape.num_rows, shape.num_layers
+    hq, hkv, d = shape.num_qo_heads, shape.num_kv_heads, shape.head_dim
+    g = torch.Generator(device=dev).manual_seed(args.seed + 7)
+    k_new = (torch.randn(nl, n, hkv, d, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    v_new = (torch.randn(nl, n, hkv, d, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    last = torch.tensor([int(wl.indices[int(wl.cu_k[i + 1]) - 1]) for i in range(n)],
+                        dtype=torch.int32, device=dev)
+    indices = wl.indices.to(dev)
+    cu_k = wl.cu_k.to(dev)
+    cu_q = torch.arange(n + 1, dtype=torch.int32)
+    t_plan = time.perf_counter()
+    plan = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=shape.prefix_len,
+                      prefix_chunk_len=args.chunk)
+    plan_us = (time.perf_counter() - t_plan) * 1e6
+    ws = torch.empty(max(plan.ws_bytes, 256), dtype=torch.uint8, device=dev)
+    out = torch.empty(nl, n, hq, d, dtype=torch.bfloat16, device=dev)
+    plan_casc = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=shape.prefix_len,
+                           prefix_chunk_len=args.chunk)
+    plan_casc.stage_mask = 1  # main launch: prefix chunks + suffix items
+    plan_rest = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=shape.prefix_len,
+                           prefix_chunk_len=args.chunk)
+    plan_rest.stage_mask = 2  # combine
+
+    stream = torch.cuda.current_stream(dev)
+    ev = []  # (start, end) around every cascade launch of the timed region
+
+    def step(record: bool):
+        for layer in range(nl):
+            store_cache(wl.k_cache[layer], wl.v_cache[layer], last, k_new[layer], v_new[layer])
+            if record:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+            paged.decode(plan_casc, wl.q[layer], wl.k_cache[layer], wl.v_cache[layer], indices, cu_k,
+                         out=out[layer], workspace=ws)
+            if record:
+                e1.record(stream)
+                ev.append((e0, e1))
+            paged.decode(plan_rest, wl.q[layer], wl.k_cache[layer], wl.v_cache[layer], indices, cu_k,
+                         out=out[layer], workspace=ws)
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    casc_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+
+    # Untimed check of the last step against a split-free recomputation.
+    plan_all = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=0)
+    ws2 = torch.empty(max(plan_all.ws_bytes, 256), dtype=torch.uint8, device=dev)
+    ref0 = paged.decode(plan_all, wl.q[0], wl.k_cache[0], wl.v_cache[0], indices, cu_k, workspace=ws2)
+    torch.cuda.synchronize()
+    max_diff = float((ref0.float() - out[0].float()).abs().max())
+
+    b_kv = 2 * hkv * d * 2
+    # Main launch: prefix K/V once, every row's suffix K/V, Q and the page ids.
+    sum_s = sum(wl.suffix_lens)
+    casc_bytes = (shape.prefix_len + sum_s) * b_kv + n * hq * d * 2 + 4 * (shape.prefix_len + sum_s)
+    casc_gbps = casc_bytes / (casc_ms * 1e-3) / 1e9
+    layer_bytes = decode_bytes_per_layer(shape, wl.suffix_lens) + kv_append_bytes(n, hkv * d)
+    step_gbps = layer_bytes * nl / (ms_per_step * 1e-3) / 1e9
+
+    result = {
+        "metric": "decode-step us & HBM GB/s (% roofline); CandidateGroup Top-3 p50 ms, 1 GPU",
+        "value": round(ms_per_step * 1e3, 2),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{shape.name} decode step: {nl} layers x (KV append + shared-prefix cascade + "
+                         f"suffix/combine), {hq}q/{hkv}kv D{d}, prefix {shape.prefix_len}, "
+                         f"{n} rows, suffix U{{0..{shape.max_suffix}}}+1, {shape.num_pages}-page pool"),
+            "seed": args.seed,
+            "prefix_chunks": plan.num_prefix_chunks,
+            "prefix_chunk_len": plan.prefix_chunk_len,
+            "suffix_splits": plan.num_suffix_splits,
+            "parts": plan.num_parts,
+        },
+        "candidate_tokens_per_s": round(n / (ms_per_step * 1e-3), 1),
+        "step_hbm_gbps": round(step_gbps, 1),
+        "step_roofline_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
+        "plan_host_us": round(plan_us, 1),
+        "check_max_abs_diff_vs_unshared": max_diff,
+        "roofline": {
+            "kernel": "decode_main_kernel<128,4,8> (prefix chunks + suffix items)",
+            "bound": "hbm",
+            "achieved": round(casc_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(casc_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": _traffic("cascade"),
+            "algorithmic_bytes_per_launch": casc_bytes,
+            "avg_launch_us": round(casc_ms * 1e3, 3),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

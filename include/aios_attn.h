@@ -82,26 +82,26 @@ typedef struct aios_attn_plan {
   int32_t total_kv;
   int32_t max_q_len;
   int32_t max_kv_len;
-  /* decode: shared-prefix cascade */
-  int32_t prefix_len;
-  int32_t prefix_chunk_len;
+  /* decode */
+  int32_t prefix_len;        /* shared prefix read once per kv-head (0 = not used) */
+  int32_t prefix_chunk_len;  /* KV positions per prefix workgroup */
   int32_t num_prefix_chunks;
-  int32_t cascade_rows;
-  int32_t cascade_waves;
-  int32_t cascade_mgroups;
-  /* decode: per-row ragged suffix */
-  int32_t suffix_split_len;
-  int32_t num_suffix_splits;
+  int32_t cascade_rows;      /* batch_size * group */
+  int32_t cascade_mgroups;   /* 128-row groups of cascade_rows */
+  int32_t suffix_split_len;  /* KV positions per suffix item */
+  int32_t num_suffix_splits; /* suffix items per (row, kv-head) */
+  int32_t suffix_tpg;        /* KV positions per DPP row per pass (8 or 16) */
+  int32_t num_parts;         /* partial states per (row, kv-head); 1 = direct output */
   /* prefill */
-  int32_t prefill_q_tile;
-  int32_t prefill_waves;
+  int32_t prefill_q_tile;    /* query tokens per workgroup */
   int32_t num_q_tiles;
-  int32_t reserved0;
+  /* decode launches to issue: bit 0 the main kernel (prefix chunks and
+   * suffix items), bit 1 the combine; 0 (the value aios_attn_plan writes)
+   * issues both.  Lets a profiler bracket the two launches separately. */
+  int32_t stage_mask;
   /* workspace layout (byte offsets) */
-  int64_t ws_prefix_o;
-  int64_t ws_prefix_lse;
-  int64_t ws_suffix_o;
-  int64_t ws_suffix_lse;
+  int64_t ws_parts_o;
+  int64_t ws_parts_lse;
   int64_t ws_bytes;
 } aios_attn_plan_t;
 

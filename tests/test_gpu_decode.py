@@ -46,10 +46,17 @@ def _oracle(wl, layer=0, rows=None):
     return ref
 
 
-def test_op_test_config_cascade():
+def test_op_test_config_default_plan():
     wl = make_decode_workload(OP_TEST, seed=20260814)
     out, p = _run(wl)
-    assert p.prefix_len == 24 and p.num_prefix_chunks >= 1
+    assert p.num_parts == 1  # short prefix: one launch, rows read it directly
+    np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
+
+
+def test_op_test_config_cascade():
+    wl = make_decode_workload(OP_TEST, seed=20260814)
+    out, p = _run(wl, chunk=32)
+    assert p.prefix_len == 24 and p.num_prefix_chunks == 1
     np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
 
 
@@ -63,7 +70,8 @@ def test_op_test_config_without_shared_prefix():
 @pytest.mark.parametrize("seed", [1, 2, 3])
 def test_cascade_and_plain_paths_agree(seed):
     wl = make_decode_workload(OP_TEST, seed=seed)
-    a, _ = _run(wl)
+    a, pa = _run(wl, chunk=32)
+    assert pa.prefix_len == 24
     b, _ = _run(wl, shared=0)
     ref = _oracle(wl)
     np.testing.assert_allclose(to_np64(a), ref, **BF16_TOL)
@@ -75,7 +83,8 @@ def test_all_suffixes_empty():
     shape = DecodeShape("empty_suffix", 1, 8, 40, 0, 8, 2, 96, 256)
     wl = make_decode_workload(shape, seed=5)
     assert all(s == 0 for s in wl.suffix_lens)
-    out, _ = _run(wl)
+    out, p = _run(wl, chunk=32)
+    assert p.prefix_len == 40
     np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
     # every row attends to the same prefix with its own query
     out0, _ = _run(wl, shared=0)
@@ -99,10 +108,13 @@ def test_forced_chunking_and_splits(chunk, split):
 def test_head_shapes(hq, hkv, d):
     shape = DecodeShape(f"h{hq}_{hkv}_{d}", 1, 8, 75, 20, hq, hkv, d, 512)
     wl = make_decode_workload(shape, seed=hq * 100 + d)
+    ref = _oracle(wl)
     out, _ = _run(wl)
-    np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
+    np.testing.assert_allclose(to_np64(out), ref, **BF16_TOL)
     out0, _ = _run(wl, shared=0)
-    np.testing.assert_allclose(to_np64(out0), _oracle(wl), **BF16_TOL)
+    np.testing.assert_allclose(to_np64(out0), ref, **BF16_TOL)
+    out1, _ = _run(wl, chunk=32)
+    np.testing.assert_allclose(to_np64(out1), ref, **BF16_TOL)
 
 
 def test_single_row_and_kv_len_one():
@@ -118,7 +130,7 @@ def test_single_row_and_kv_len_one():
 def test_many_rows_multiple_mgroups():
     shape = DecodeShape("wide", 1, 48, 96, 12, 16, 4, 64, 2048)  # M = 48*4 = 192 rows
     wl = make_decode_workload(shape, seed=21)
-    out, p = _run(wl)
+    out, p = _run(wl, chunk=32)
     assert p.cascade_mgroups == 2
     np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
 
@@ -143,3 +155,22 @@ def test_page_permutation_invariance():
     wl.indices = inv[wl.indices.long()].to(torch.int32)
     out2, _ = _run(wl)
     assert torch.equal(out.cpu(), out2.cpu())
+
+
+def test_long_rows_without_shared_prefix():
+    # Generic paged decode (no shared prefix): long rows are split and merged.
+    shape = DecodeShape("long_rows", 1, 3, 0, 3000, 16, 8, 128, 16384, min_suffix=1500)
+    wl = make_decode_workload(shape, seed=31)
+    out, p = _run(wl, shared=0)
+    assert p.num_suffix_splits > 1 and p.num_parts > 1
+    np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
+
+
+@pytest.mark.parametrize("max_suffix", [33, 64, 65])
+def test_single_launch_row_lengths(max_suffix):
+    # Rows of up to 64 positions are covered by one suffix item (16 per DPP row).
+    shape = DecodeShape("rows", 1, 6, 0, max_suffix, 8, 2, 96, 512, min_suffix=max_suffix)
+    wl = make_decode_workload(shape, seed=max_suffix)
+    out, p = _run(wl, shared=0)
+    assert (p.num_parts == 1) == (max_suffix <= 64)
+    np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)

@@ -34,8 +34,8 @@ def test_library_exports_every_symbol():
 
 
 def test_plan_struct_layout_matches_header():
-    # 22 int32 fields followed by 5 int64 fields.
-    assert ctypes.sizeof(_lib.AttnPlan) == 22 * 4 + 5 * 8
+    # 22 int32 fields followed by 3 int64 fields.
+    assert ctypes.sizeof(_lib.AttnPlan) == 22 * 4 + 3 * 8
 
 
 def _plan(phase, cu_q, cu_k, hq=8, hkv=2, d=96, shared=0, ws=1 << 26, chunk=0, split=0):
@@ -47,13 +47,39 @@ def _plan(phase, cu_q, cu_k, hq=8, hkv=2, d=96, shared=0, ws=1 << 26, chunk=0, s
     return rc, p
 
 
-def test_plan_decode_shared_prefix_schedule():
+def test_plan_decode_short_prefix_reads_per_row():
+    # Op-test shape: a 24-token prefix is cheaper to read per row in one launch.
     kv = [24 + s for s in (3, 0, 16, 7, 1, 9, 12, 5)]
     rc, p = _plan(_lib.PHASE_DECODE, np.arange(9), np.cumsum([0] + kv), shared=24)
     assert rc == 0
-    assert p.prefix_len == 24 and p.cascade_rows == 32 and p.cascade_waves == 1
-    assert p.num_suffix_splits == 1
-    assert p.ws_bytes >= p.num_prefix_chunks * 2 * 32 * 97 * 4
+    assert p.prefix_len == 0 and p.num_parts == 1 and p.ws_bytes == 0
+    assert p.num_suffix_splits == 1 and p.suffix_split_len >= max(kv)
+
+
+def test_plan_decode_forced_cascade():
+    kv = [24 + s for s in (3, 0, 16, 7, 1, 9, 12, 5)]
+    rc, p = _plan(_lib.PHASE_DECODE, np.arange(9), np.cumsum([0] + kv), shared=24, chunk=32)
+    assert rc == 0
+    assert p.prefix_len == 24 and p.num_prefix_chunks == 1 and p.cascade_rows == 32
+    assert p.num_parts == p.num_prefix_chunks + p.num_suffix_splits
+    assert p.ws_bytes >= 8 * 2 * p.num_parts * 4 * 96 * 4
+
+
+def test_plan_decode_long_context_schedule():
+    kv = [4096 + 1 + s for s in range(0, 65, 3)][:24]
+    kv += [4096] * (24 - len(kv))
+    rc, p = _plan(_lib.PHASE_DECODE, np.arange(25), np.cumsum([0] + kv), hq=32, hkv=8, d=128,
+                  shared=4096)
+    assert rc == 0
+    assert p.prefix_len == 4096 and p.cascade_rows == 96 and p.cascade_mgroups == 1
+    assert p.num_prefix_chunks * p.prefix_chunk_len >= 4096
+    assert p.num_parts <= 64
+
+
+def test_plan_decode_long_rows_without_prefix_split():
+    rc, p = _plan(_lib.PHASE_DECODE, np.arange(3), np.cumsum([0, 3000, 17]), shared=0)
+    assert rc == 0
+    assert p.prefix_len == 0 and p.num_suffix_splits > 1 and p.num_parts <= 64
 
 
 def test_plan_rejects_bad_batches():
@@ -83,7 +109,7 @@ def test_plan_prefill_tiles_cover_queries():
     rc, p = _plan(_lib.PHASE_PREFILL, [0, 4096], [0, 4096], hq=32, hkv=8, d=128)
     assert rc == 0
     assert p.num_q_tiles * p.prefill_q_tile >= 4096
-    assert p.prefill_q_tile * 4 <= p.prefill_waves * 32
+    assert p.prefill_q_tile * 4 <= 128
 
 
 def test_check_maps_status_to_exceptions():
