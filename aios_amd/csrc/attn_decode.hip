@@ -65,6 +65,7 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
   const int h = unit / a.n_chunks;
 
   TileEngine<D, false> eng;
+  eng.min_limit = 0x7fffffff;
   int rows[2];
   bool ok[2];
   const bf16* qr[2];

@@ -45,6 +45,7 @@ __global__ __launch_bounds__(kEngineThreads) void prefill_kernel(PrefillArgs a) 
     out_off[rt] = ((int64_t)(q_start + i) * a.num_qo_heads + (h * G + g)) * D;
     eng.limit[rt] = cached + i;
   }
+  eng.min_limit = cached + qt * a.q_tile;
   eng.load_q(qr[0], ok[0], qr[1], ok[1]);
   eng.run(lds, reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2,
           reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2, a.kv_tok_stride * 2,

@@ -38,6 +38,8 @@ constexpr int kSubTok = 32;       // KV positions per sub-tile
 constexpr int kRing = 4;          // sub-tiles in the LDS ring
 constexpr int kIdWindow = 1024;   // page ids staged in LDS at a time
 constexpr int kEngineThreads = 256;
+// The softmax reference may lag a row's running max by up to 2^8.
+constexpr float kRescaleSlack = 8.0f;
 
 // Source of every masked / out-of-range K or V chunk.
 static __device__ __align__(16) uint8_t g_zero_kv_row[512] = {0};
@@ -88,7 +90,8 @@ struct TileEngine {
   f32x4 o[2][DTILES];
   float m_run[2];
   float l_run[2];
-  int limit[2];  // CAUSAL: last visible KV position of the lane's rows
+  int limit[2];    // CAUSAL: last visible KV position of the lane's rows
+  int min_limit;   // CAUSAL: smallest limit of any row of the workgroup
 
   // Q fragment (B operand of S^T = K Q^T) of the lane's two rows.
   __device__ __forceinline__ void load_q(const bf16* q0, bool ok0, const bf16* q1, bool ok1) {
@@ -200,6 +203,10 @@ struct TileEngine {
       }
     }
 
+    // Online softmax with a lazily moved reference: m_run only moves when a
+    // row's scaled max exceeds it by more than kRescaleSlack (p <= 2^slack
+    // otherwise), so the O rescale below is skipped once the max settles.
+    const bool full = kv0 + kSubTok <= kv_end && (!CAUSAL || kv0 + kSubTok - 1 <= min_limit);
     bf16x8 pb[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
@@ -207,30 +214,39 @@ struct TileEngine {
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int pos = kv0 + tt * 16 + lg * 4 + i;
-          bool ok = pos < kv_end;
-          if (CAUSAL) ok = ok && pos <= limit[rt];
-          x[tt * 4 + i] = ok ? st[rt][tt][i] * scale_log2 : kNegInf;
-        }
-      float mx = x[0];
+        for (int i = 0; i < 4; ++i) x[tt * 4 + i] = st[rt][tt][i];
+      if (!full) {
 #pragma unroll
-      for (int j = 1; j < 8; ++j) mx = fmaxf(mx, x[j]);
-      mx = xrow_max(mx);
-      const float m_new = fmaxf(m_run[rt], mx);
-      const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run[rt] - m_use);
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int pos = kv0 + tt * 16 + lg * 4 + i;
+            bool ok = pos < kv_end;
+            if (CAUSAL) ok = ok && pos <= limit[rt];
+            if (!ok) x[tt * 4 + i] = kNegInf;
+          }
+      }
+      float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                       fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+      mx = xrow_max(mx) * scale_log2;
+      const bool need = mx > m_run[rt] + kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(need)) {
+        const float m_new = need ? mx : m_run[rt];
+        const float alpha = fast_exp2(m_run[rt] - m_new);  // 0 when m_run is -inf
+        l_run[rt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] *= alpha;
+        m_run[rt] = m_new;
+      }
+      const float m_use = (m_run[rt] == kNegInf) ? 0.f : m_run[rt];
       float p[8];
       float psum = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        p[j] = fast_exp2(x[j] - m_use);
+        p[j] = fast_exp2(fmaf(x[j], scale_log2, -m_use));
         psum += p[j];
       }
-      l_run[rt] = l_run[rt] * alpha + psum;
-      m_run[rt] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] *= alpha;
+      l_run[rt] += psum;
       pb[rt] = __builtin_bit_cast(
           bf16x8, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
                              pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])));

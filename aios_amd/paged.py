@@ -138,3 +138,62 @@ def build_indices(page_table: torch.Tensor, row_ids: torch.Tensor, cu_k: torch.T
         "aios_build_indices",
     )
     return out
+
+
+class BoundCall:
+    """A C-ABI launch with its arguments converted once.
+
+    For loops that replay the same launch on fixed buffers (benchmarks, graph
+    capture): calling the bound function skips the per-call tensor checks and
+    ctypes conversions of :func:`decode` / :func:`prefill`.
+    """
+
+    def __init__(self, fn, args, keep):
+        self._fn = fn
+        self._args = args
+        self._keep = keep  # tensors and plans the pointers refer to
+
+    def __call__(self) -> None:
+        _lib.check(self._fn(*self._args), self._fn.__name__)
+
+
+def bind_decode(p: _lib.AttnPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                indices: torch.Tensor, cu_k: torch.Tensor, out: torch.Tensor,
+                workspace: torch.Tensor | None, sm_scale: float | None = None,
+                stream: torch.cuda.Stream | None = None) -> BoundCall:
+    """Checked once, then launched many times on the same buffers."""
+    import ctypes
+
+    _check_q(q, p)
+    _check_cache(k_cache, p)
+    _check_cache(v_cache, p)
+    _check_i32(indices, "indices", p.total_kv)
+    _check_i32(cu_k, "cu_k", p.batch_size + 1)
+    if out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like q")
+    if p.ws_bytes and (workspace is None or workspace.numel() < p.ws_bytes):
+        raise RuntimeError(f"decode needs a workspace of {p.ws_bytes} bytes")
+    scale = p.head_dim ** -0.5 if sm_scale is None else sm_scale
+    s = stream.cuda_stream if stream is not None else _stream(q.device)
+    args = (ctypes.byref(p), q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+            k_cache.shape[0], indices.data_ptr(), cu_k.data_ptr(), out.data_ptr(),
+            workspace.data_ptr() if workspace is not None else None,
+            workspace.numel() if workspace is not None else 0, ctypes.c_float(scale), s)
+    return BoundCall(_lib.lib().aios_attn_decode, args,
+                     (p, q, k_cache, v_cache, indices, cu_k, out, workspace))
+
+
+def bind_kv_append(k_cache: torch.Tensor, v_cache: torch.Tensor, out_loc: torch.Tensor,
+                   k: torch.Tensor, v: torch.Tensor,
+                   stream: torch.cuda.Stream | None = None) -> BoundCall:
+    """Checked once, then launched many times: store_cache on fixed buffers."""
+    if k_cache.ndim != 3 or k.shape[1:] != k_cache.shape[1:] or k.shape != v.shape:
+        raise ValueError("K/V input shape does not match the cache layout")
+    if out_loc.dtype != torch.int32 or not out_loc.is_contiguous() or out_loc.numel() != k.shape[0]:
+        raise ValueError("out_loc must be a contiguous int32 tensor with one entry per token")
+    s = stream.cuda_stream if stream is not None else _stream(k.device)
+    width = k_cache.shape[1] * k_cache.shape[2]
+    args = (k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0], k_cache.stride(0),
+            out_loc.data_ptr(), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), k.shape[0],
+            width, k.element_size(), s)
+    return BoundCall(_lib.lib().aios_kv_append, args, (k_cache, v_cache, out_loc, k, v))

@@ -11,7 +11,7 @@ the timed region; the per-batch plan is built once before it (it is host-only
 work done once per batch by prepare_metadata).
 
 Prints one JSON line: value = decode-step microseconds (lower is better),
-with the cascade kernel's roofline measured live with HIP events, and the
+with the main decode kernel's roofline measured live with HIP events, and the
 reference's CPU attention path (restated, oracle/sdpa_cpu.py) timed on a
 bounded sample on the host cores.
 """
@@ -146,34 +146,62 @@ def main() -> int:
                            prefix_chunk_len=args.chunk)
     plan_rest.stage_mask = 2  # combine
 
-    stream = torch.cuda.current_stream(dev)
-    ev = []  # (start, end) around every cascade launch of the timed region
+    # Every launch is bound once to fixed buffers on one stream, so a step can
+    # be captured as a HIP graph and replayed without host overhead.
+    s = torch.cuda.Stream(dev)
+    app = [paged.bind_kv_append(wl.k_cache[l], wl.v_cache[l], last, k_new[l], v_new[l], stream=s)
+           for l in range(nl)]
+    main_calls = [paged.bind_decode(plan_casc, wl.q[l], wl.k_cache[l], wl.v_cache[l], indices, cu_k,
+                                    out[l], ws, stream=s) for l in range(nl)]
+    comb_calls = [paged.bind_decode(plan_rest, wl.q[l], wl.k_cache[l], wl.v_cache[l], indices, cu_k,
+                                    out[l], ws, stream=s) for l in range(nl)]
 
-    def step(record: bool):
+    def step():
         for layer in range(nl):
-            store_cache(wl.k_cache[layer], wl.v_cache[layer], last, k_new[layer], v_new[layer])
-            if record:
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-            paged.decode(plan_casc, wl.q[layer], wl.k_cache[layer], wl.v_cache[layer], indices, cu_k,
-                         out=out[layer], workspace=ws)
-            if record:
-                e1.record(stream)
-                ev.append((e0, e1))
-            paged.decode(plan_rest, wl.q[layer], wl.k_cache[layer], wl.v_cache[layer], indices, cu_k,
-                         out=out[layer], workspace=ws)
+            app[layer]()
+            main_calls[layer]()
+            comb_calls[layer]()
 
-    for _ in range(args.warmup):
-        step(False)
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.synchronize()
+    eager_out = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        step()
+    with torch.cuda.stream(s):
+        for _ in range(args.warmup):
+            graph.replay()
+    torch.cuda.synchronize()
+    graph_matches_eager = bool(torch.equal(out, eager_out))
+
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step(True)
+    with torch.cuda.stream(s):
+        for _ in range(args.steps):
+            graph.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
-    casc_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+
+    def per_launch_ms(calls, reps):
+        """Average duration of back-to-back launches, bracketed by HIP events on `s`."""
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            for c in calls:  # warm
+                c()
+            e0.record(s)
+            for _ in range(reps):
+                for c in calls:
+                    c()
+            e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (reps * len(calls))
+
+    casc_ms = per_launch_ms(main_calls, max(2, args.steps // 4))
+    comb_ms = per_launch_ms(comb_calls, max(2, args.steps // 4))
+    app_ms = per_launch_ms(app, max(2, args.steps // 4))
 
     # Untimed check of the last step against a split-free recomputation.
     plan_all = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=0)
@@ -217,6 +245,9 @@ def main() -> int:
         "step_hbm_gbps": round(step_gbps, 1),
         "step_roofline_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "plan_host_us": round(plan_us, 1),
+        "graph_replay_matches_eager": graph_matches_eager,
+        "kernel_us": {"decode_main": round(casc_ms * 1e3, 3), "combine": round(comb_ms * 1e3, 3),
+                      "kv_append": round(app_ms * 1e3, 3)},
         "check_max_abs_diff_vs_unshared": max_diff,
         "roofline": {
             "kernel": "decode_main_kernel<128,4,8> (prefix chunks + suffix items)",
