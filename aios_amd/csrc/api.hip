@@ -153,15 +153,15 @@ int aios_attn_plan(int32_t phase, const int32_t* cu_q, const int32_t* cu_k, int3
     n_chunks = cdiv(P, chunk);
   }
   const int32_t max_suffix = max_kv - P;
-  int32_t tpg = 8;
+  const int32_t tpg = aios::suffix_tpg(d, G);
+  const int32_t pass = 4 * tpg;  // KV positions one suffix wavefront loads at once
   int32_t split;
   if (suffix_split_len > 0) {
     split = suffix_split_len;
-  } else if (!cascade && max_suffix <= 64) {
-    tpg = max_suffix > 32 ? 16 : 8;  // one item covers the whole row
-    split = max_suffix > 0 ? max_suffix : 1;
+  } else if (!cascade && max_suffix <= 2 * pass) {
+    split = max_suffix > 0 ? max_suffix : 1;  // one item covers the whole row
   } else {
-    split = 4 * tpg;  // one pass per item
+    split = pass;
   }
   int32_t n_splits = max_suffix > 0 ? cdiv(max_suffix, split) : 1;
   // Bound the parts per (row, kv-head) merged by the combine.
@@ -186,7 +186,7 @@ int aios_attn_plan(int32_t phase, const int32_t* cu_q, const int32_t* cu_k, int3
   p->num_parts = n_parts;
   if (n_parts > 1) {
     p->ws_parts_o = 0;
-    p->ws_parts_lse = align_up((int64_t)batch * hkv * n_parts * G * d * 4, 256);
+    p->ws_parts_lse = align_up((int64_t)batch * hkv * n_parts * G * d * 2, 256);
     p->ws_bytes = p->ws_parts_lse + align_up((int64_t)batch * hkv * n_parts * G * 4, 256);
   }
   if (p->ws_bytes > ws_bytes)
@@ -292,13 +292,13 @@ int aios_attn_decode(const aios_attn_plan_t* p, const void* q, int64_t q_tok_str
   a.n_splits = p->num_suffix_splits;
   a.suffix_items = p->batch_size * p->num_kv_heads * p->num_suffix_splits;
   a.final_out = p->num_parts == 1 ? 1 : 0;
-  a.parts.o = reinterpret_cast<float*>(ws + p->ws_parts_o);
+  a.parts.o = reinterpret_cast<aios::bf16*>(ws + p->ws_parts_o);
   a.parts.lse = reinterpret_cast<float*>(ws + p->ws_parts_lse);
   a.parts.n_parts = p->num_parts;
   a.parts.n_chunks = p->num_prefix_chunks;
   a.out = static_cast<aios::bf16*>(out);
   if (mask & 1) {
-    rc = check_hip(aios::launch_decode_main(D, p->suffix_tpg, a, s), "decode launch");
+    rc = check_hip(aios::launch_decode_main(D, a, s), "decode launch");
     if (rc) return rc;
   }
   if (p->num_parts > 1 && (mask & 2))

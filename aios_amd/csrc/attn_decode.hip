@@ -89,17 +89,22 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
   constexpr int DT = D / 16;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    const float l_tot = xrow_sum(eng.l_run[rt]);
+    const float l_tot = eng.l_run[rt];
     if (!ok[rt]) continue;
     const int m = rows[rt];
     const int b = m / G;
     const int g = m - b * G;
     const int64_t slot = ((int64_t)b * a.num_kv_heads + h) * a.parts.n_parts + chunk;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    float* po = a.parts.o + (slot * G + g) * D;
+    bf16* po = a.parts.o + (slot * G + g) * D;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      *reinterpret_cast<f32x4*>(po + dt * 16 + lg * 4) = eng.o[rt][dt] * inv;
+    for (int dt = 0; dt < DT; ++dt) {
+      const f32x4 v = eng.o[rt][dt] * inv;
+      uint2 packed;
+      packed.x = pack_bf16x2(v[0], v[1]);
+      packed.y = pack_bf16x2(v[2], v[3]);
+      *reinterpret_cast<uint2*>(po + dt * 16 + lg * 4) = packed;
+    }
     if (lg == 0)
       a.parts.lse[slot * G + g] = l_tot > 0.f ? eng.m_run[rt] + fast_log2(l_tot) : kNegInf;
   }
@@ -240,23 +245,24 @@ __device__ __forceinline__ void decode_suffix_item(const DecodeArgs& a, int item
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
-      float* po = a.parts.o + (slot * G + g) * D + l16 * E;
+      uint32_t* pw = reinterpret_cast<uint32_t*>(a.parts.o + (slot * G + g) * D + l16 * E);
 #pragma unroll
-      for (int e = 0; e < E; ++e) po[e] = acc[g][e] * inv;
+      for (int i = 0; i < E / 2; ++i)
+        pw[i] = pack_bf16x2(acc[g][2 * i] * inv, acc[g][2 * i + 1] * inv);
       if (l16 == 0) a.parts.lse[slot * G + g] = l[g] > 0.f ? m[g] + fast_log2(l[g]) : kNegInf;
     }
   }
 }
 
-template <int D, int G, int TPG>
-__global__ __launch_bounds__(kEngineThreads) void decode_main_kernel(DecodeArgs a) {
+template <int D, int G>
+__global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_main_kernel(DecodeArgs a) {
   __shared__ __align__(16) uint8_t lds[KVTile<D>::LDS_BYTES];
   const int wg = blockIdx.x;
   if (wg < a.prefix_wgs) {
     decode_prefix_part<D>(lds, a, wg);
   } else {
     const int item = (wg - a.prefix_wgs) * (kEngineThreads / 64) + (threadIdx.x >> 6);
-    if (item < a.suffix_items) decode_suffix_item<D, G, TPG>(a, item);
+    if (item < a.suffix_items) decode_suffix_item<D, G, suffix_tpg(D, G)>(a, item);
   }
 }
 
@@ -282,7 +288,7 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
   const int h = bh - b * a.num_kv_heads;
   const int np = a.parts.n_parts;
   const int64_t base = (int64_t)bh * np;
-  const f32x4* po = reinterpret_cast<const f32x4*>(a.parts.o + base * G * D);
+  const uint2* po = reinterpret_cast<const uint2*>(a.parts.o + base * G * D);  // 4 bf16 per element
   const float* pl = a.parts.lse + base * G;
   const int e = tid % E4;
   const int r = tid / E4;
@@ -290,11 +296,11 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
   const int g = (e * 4) / D;
 
   // Issue this thread's o loads first (independent of the weights).
-  f32x4 v[kCombineBatch];
+  uint2 v[kCombineBatch];
 #pragma unroll
   for (int k = 0; k < kCombineBatch; ++k) {
     const int j = r + k * R;
-    v[k] = (active && j < np) ? po[(int64_t)j * E4 + e] : f32x4{0.f, 0.f, 0.f, 0.f};
+    v[k] = (active && j < np) ? po[(int64_t)j * E4 + e] : make_uint2(0, 0);
   }
   for (int i = tid; i < np * G; i += kCombineThreads) lse_s[i] = pl[i];
   __syncthreads();
@@ -312,21 +318,25 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   if (active) {
     const float mu = mx_s[g];
+    auto fold = [&](int j, uint2 w) {
+      const float f = fast_exp2(lse_s[j * G + g] - mu);
+      acc += f32x4{lo_bf16(w.x), hi_bf16(w.x), lo_bf16(w.y), hi_bf16(w.y)} * f;
+    };
 #pragma unroll
     for (int k = 0; k < kCombineBatch; ++k) {
       const int j = r + k * R;
-      if (j < np) acc += v[k] * fast_exp2(lse_s[j * G + g] - mu);
+      if (j < np) fold(j, v[k]);
     }
     for (int j0 = r + kCombineBatch * R; j0 < np; j0 += kCombineBatch * R) {
 #pragma unroll
       for (int k = 0; k < kCombineBatch; ++k) {
         const int j = j0 + k * R;
-        v[k] = j < np ? po[(int64_t)j * E4 + e] : f32x4{0.f, 0.f, 0.f, 0.f};
+        v[k] = j < np ? po[(int64_t)j * E4 + e] : make_uint2(0, 0);
       }
 #pragma unroll
       for (int k = 0; k < kCombineBatch; ++k) {
         const int j = j0 + k * R;
-        if (j < np) acc += v[k] * fast_exp2(lse_s[j * G + g] - mu);
+        if (j < np) fold(j, v[k]);
       }
     }
   }
@@ -353,35 +363,32 @@ bool group_supported(int G) {
 }
 
 template <int D, int G>
-static hipError_t launch_main_dg(int tpg, const DecodeArgs& a, hipStream_t s) {
-  const int suffix_wgs = (a.suffix_items + 3) / 4;
+static hipError_t launch_main_dg(const DecodeArgs& a, hipStream_t s) {
+  const int suffix_wgs = (a.suffix_items + kEngineThreads / 64 - 1) / (kEngineThreads / 64);
   const dim3 grid(a.prefix_wgs + suffix_wgs);
   if (grid.x == 0) return hipSuccess;
-  if (tpg == 16)
-    hipLaunchKernelGGL((decode_main_kernel<D, G, 16>), grid, dim3(kEngineThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL((decode_main_kernel<D, G, 8>), grid, dim3(kEngineThreads), 0, s, a);
+  hipLaunchKernelGGL((decode_main_kernel<D, G>), grid, dim3(kEngineThreads), 0, s, a);
   return hipGetLastError();
 }
 
 template <int D>
-static hipError_t launch_main_d(int tpg, const DecodeArgs& a, hipStream_t s) {
+static hipError_t launch_main_d(const DecodeArgs& a, hipStream_t s) {
   switch (a.group) {
-    case 1: return launch_main_dg<D, 1>(tpg, a, s);
-    case 2: return launch_main_dg<D, 2>(tpg, a, s);
-    case 3: return launch_main_dg<D, 3>(tpg, a, s);
-    case 4: return launch_main_dg<D, 4>(tpg, a, s);
-    case 6: return launch_main_dg<D, 6>(tpg, a, s);
-    case 8: return launch_main_dg<D, 8>(tpg, a, s);
+    case 1: return launch_main_dg<D, 1>(a, s);
+    case 2: return launch_main_dg<D, 2>(a, s);
+    case 3: return launch_main_dg<D, 3>(a, s);
+    case 4: return launch_main_dg<D, 4>(a, s);
+    case 6: return launch_main_dg<D, 6>(a, s);
+    case 8: return launch_main_dg<D, 8>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t launch_decode_main(int D, int tpg, const DecodeArgs& a, hipStream_t s) {
+hipError_t launch_decode_main(int D, const DecodeArgs& a, hipStream_t s) {
   switch (D) {
-    case 64: return launch_main_d<64>(tpg, a, s);
-    case 96: return launch_main_d<96>(tpg, a, s);
-    case 128: return launch_main_d<128>(tpg, a, s);
+    case 64: return launch_main_d<64>(a, s);
+    case 96: return launch_main_d<96>(a, s);
+    case 128: return launch_main_d<128>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -13,7 +13,7 @@
 namespace aios {
 
 template <int D>
-__global__ __launch_bounds__(kEngineThreads) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PrefillArgs a) {
   __shared__ __align__(16) uint8_t lds[KVTile<D>::LDS_BYTES];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(kEngineThreads) void prefill_kernel(PrefillArgs a) 
   constexpr int DT = D / 16;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    const float l_tot = xrow_sum(eng.l_run[rt]);
+    const float l_tot = eng.l_run[rt];
     if (!ok[rt]) continue;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     bf16* po = a.out + out_off[rt];

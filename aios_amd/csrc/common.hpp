@@ -56,16 +56,28 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
-// Cross-row (lanes l, l^16, l^32, l^48) reductions.
-__device__ __forceinline__ float xrow_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+// Cross-row (lanes l, l^16, l^32, l^48) reductions with the gfx950 lane
+// swaps: v_permlane16_swap exchanges the odd 16-lane rows of its first
+// operand with the even rows of its second, v_permlane32_swap the upper and
+// lower halves; with both operands equal to x, the two results of a swap
+// hold x[l] and x[l ^ 16] (resp. x[l ^ 32]) in some order on every lane.
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ __forceinline__ float xrow_sum(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xrow_max(float x) { return xor32_max(xor16_max(x)); }
+__device__ __forceinline__ float xrow_sum(float x) { return xor32_sum(xor16_sum(x)); }
 
 }  // namespace aios

@@ -9,16 +9,18 @@
 // Data movement: the range's page ids are staged in LDS, then K/V rows are
 // gathered page by page straight from HBM into an LDS ring of four 32-token
 // sub-tiles with global_load_lds_dwordx4 (no VGPR staging), three sub-tiles
-// ahead of the one being consumed.  Rows are stored token-major with the
-// sixteen-byte chunks of each row rotated (K by the token index, V by twice
-// the token index) so that both MFMA operand reads below are bank-conflict
-// free.  Masked or out-of-range positions load a zero row.
+// ahead of the one being consumed.  Rows are stored token-major with the sixteen-byte
+// chunks of each row rotated (K by the token index, V by twice the token
+// index) so that both MFMA operand reads below are bank-conflict free.
+// Masked or out-of-range positions load a zero row.
 //
 // Math per 32-token sub-tile and wavefront:
 //   S^T = K Q^T         v_mfma_f32_16x16x32_bf16, A = K rows (ds_read_b128),
 //                       B = Q fragments kept in registers
 //   online softmax      one query row per lane column; row max over the four
-//                       lane groups by cross-row shuffles; log2 domain
+//                       lane groups by v_permlane16/32_swap; log2 domain; the
+//                       reference max moves only when a row's max grows by
+//                       more than 2^8, so O is rarely rescaled
 //   O^T += V^T P^T      A = V^T read with ds_read_b64_tr_b16 (the LDS
 //                       transpose read) from the token-major V rows, B = P^T,
 //                       which is exactly the fragment each lane holds after
@@ -105,8 +107,8 @@ struct TileEngine {
 
   // Stream KV positions [kv_begin, kv_end) of one kv-head (kc / vc point at
   // head h of page 0; tok_bytes = page stride) whose page ids are
-  // idx[kv_begin .. kv_end).  Leaves o (unnormalised), m_run and the
-  // lane-partial l_run.
+  // idx[kv_begin .. kv_end).  Leaves o (unnormalised), m_run and the row
+  // total l_run.
   __device__ void run(uint8_t* lds, const uint8_t* kc, const uint8_t* vc, int64_t tok_bytes,
                       int64_t num_pages, const int32_t* idx, int kv_begin, int kv_end,
                       float scale_log2) {
@@ -136,24 +138,39 @@ struct TileEngine {
     stage_ids();
     lds_barrier();
 
+    // Loop-invariant part of every DMA load of this thread: which token of
+    // the sub-tile it serves, and the byte offset (rotated chunk) inside that
+    // token's K or V row.  Per-layer caches are below 4 GiB, so page offsets
+    // are 32-bit.
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    int tok_j[T::LPS];
+    uint32_t coff_j[T::LPS];
+    bool isv_j[T::LPS];
+#pragma unroll
+    for (int j = 0; j < T::LPS; ++j) {
+      const int off = (j * kEngineThreads + tid) * 16;
+      const bool isv = off >= T::SUB_KB;
+      const int o2 = isv ? off - T::SUB_KB : off;
+      const int t = o2 / T::ROWB;
+      const int slot = (o2 - t * T::ROWB) >> 4;
+      tok_j[j] = t;
+      isv_j[j] = isv;
+      coff_j[j] = (uint32_t)((isv ? T::v_chunk(t, slot) : T::k_chunk(t, slot)) * 16);
+    }
+    const uint32_t tok_b = (uint32_t)tok_bytes;
+    const uint32_t n_pages = (uint32_t)num_pages;
     auto issue = [&](int s) {
       uint8_t* buf = lds + (s & (kRing - 1)) * T::SUB_BYTES;
       const int pos0 = kv_begin + s * kSubTok;
 #pragma unroll
       for (int j = 0; j < T::LPS; ++j) {
-        const int off = (j * kEngineThreads + tid) * 16;
-        const bool isv = off >= T::SUB_KB;
-        const int o2 = isv ? off - T::SUB_KB : off;
-        const int t = o2 / T::ROWB;
-        const int slot = (o2 - t * T::ROWB) >> 4;
-        const int c = isv ? T::v_chunk(t, slot) : T::k_chunk(t, slot);
-        const int gp = pos0 + t;
-        const int64_t page = gp < kv_end ? (int64_t)ids[gp - win] : -1;
-        const uint8_t* src = ((uint64_t)page < (uint64_t)num_pages)
-                                 ? (isv ? vc : kc) + page * tok_bytes + c * 16
-                                 : g_zero_kv_row + c * 16;
+        const int gp = pos0 + tok_j[j];
+        const uint32_t page = gp < kv_end ? (uint32_t)ids[gp - win] : 0xffffffffu;
+        const uint8_t* src = page < n_pages
+                                 ? (isv_j[j] ? vc : kc) + (page * tok_b + coff_j[j])
+                                 : g_zero_kv_row + coff_j[j];
         __builtin_amdgcn_global_load_lds(
-            src, (AIOS_LDS void*)(buf + (j * kEngineThreads + wave * 64) * 16), 16, 0, 0);
+            src, (AIOS_LDS void*)(buf + (j * kEngineThreads + wave_u * 64) * 16), 16, 0, 0);
       }
     };
 
@@ -182,39 +199,71 @@ struct TileEngine {
       compute(lds + (it & (kRing - 1)) * T::SUB_BYTES, kv_begin + it * kSubTok, kv_end,
               scale_log2, l16, lg);
     }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) l_run[rt] = xrow_sum(l_run[rt]);
   }
 
   __device__ __forceinline__ void compute(const uint8_t* kb, int kv0, int kv_end, float scale_log2,
                                           int l16, int lg) {
     const uint8_t* vb = kb + T::SUB_KB;
-    // S^T tiles: st[rt][tt][i] = S[row rt*16 + l16][token tt*16 + lg*4 + i]
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    // Issue every LDS operand read of the sub-tile before the first MFMA so
+    // their latencies overlap: K rows (A of S^T) and the V^T fragments (A of
+    // O^T, transpose reads; consumed after the softmax).
+    bf16x8 kf[2][KSTEPS];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int t = tt * 16 + l16;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+        kf[tt][s] = *reinterpret_cast<const bf16x8*>(kb + t * T::ROWB +
+                                                      T::k_slot(t, s * 4 + lg) * 16);
+    }
+    bf16x4 va[DTILES][2];
+    {
+      const int r = l16 >> 2;
+      const int q4 = l16 & 3;
+      const int t0 = lg * 4 + r;
+      const int t1 = 16 + lg * 4 + r;
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) {
+        const int dim = dt * 16 + 4 * q4;
+        const int c = dim >> 3;
+        const int boff = (dim & 7) * 2;
+        va[dt][0] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (AIOS_LDS bf16x4*)(vb + t0 * T::ROWB + T::v_slot(t0, c) * 16 + boff));
+        va[dt][1] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (AIOS_LDS bf16x4*)(vb + t1 * T::ROWB + T::v_slot(t1, c) * 16 + boff));
+      }
+    }
+    // S^T tiles: st[rt][tt][i] = S[row rt*16 + l16][token tt*16 + lg*4 + i];
+    // the four accumulation chains are interleaved.
     f32x4 st[2][2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       st[0][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
       st[1][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int t = tt * 16 + l16;
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kb + t * T::ROWB +
-                                                           T::k_slot(t, s * 4 + lg) * 16);
-        st[0][tt] = mfma16x16x32(kf, qf[0][s], st[0][tt]);
-        st[1][tt] = mfma16x16x32(kf, qf[1][s], st[1][tt]);
-      }
     }
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        st[0][tt] = mfma16x16x32(kf[tt][s], qf[0][s], st[0][tt]);
+        st[1][tt] = mfma16x16x32(kf[tt][s], qf[1][s], st[1][tt]);
+      }
 
     // Online softmax with a lazily moved reference: m_run only moves when a
     // row's scaled max exceeds it by more than kRescaleSlack (p <= 2^slack
     // otherwise), so the O rescale below is skipped once the max settles.
     const bool full = kv0 + kSubTok <= kv_end && (!CAUSAL || kv0 + kSubTok - 1 <= min_limit);
-    bf16x8 pb[2];
+    float x[2][8];
+    float mx[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      float x[8];
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[tt * 4 + i] = st[rt][tt][i];
+        for (int i = 0; i < 4; ++i) x[rt][tt * 4 + i] = st[rt][tt][i];
       if (!full) {
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
@@ -223,27 +272,42 @@ struct TileEngine {
             const int pos = kv0 + tt * 16 + lg * 4 + i;
             bool ok = pos < kv_end;
             if (CAUSAL) ok = ok && pos <= limit[rt];
-            if (!ok) x[tt * 4 + i] = kNegInf;
+            if (!ok) x[rt][tt * 4 + i] = kNegInf;
           }
       }
-      float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
-                       fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-      mx = xrow_max(mx) * scale_log2;
-      const bool need = mx > m_run[rt] + kRescaleSlack;
-      if (__builtin_amdgcn_ballot_w64(need)) {
-        const float m_new = need ? mx : m_run[rt];
-        const float alpha = fast_exp2(m_run[rt] - m_new);  // 0 when m_run is -inf
-        l_run[rt] *= alpha;
+      mx[rt] = fmaxf(fmaxf(fmaxf(x[rt][0], x[rt][1]), fmaxf(x[rt][2], x[rt][3])),
+                     fmaxf(fmaxf(x[rt][4], x[rt][5]), fmaxf(x[rt][6], x[rt][7])));
+    }
+    mx[0] = xrow_max(mx[0]) * scale_log2;
+    mx[1] = xrow_max(mx[1]) * scale_log2;
+    const bool need0 = mx[0] > m_run[0] + kRescaleSlack;
+    const bool need1 = mx[1] > m_run[1] + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(need0 || need1)) {
+      // Rows that keep their reference use alpha = 1 exactly (their reference
+      // may still be -inf); a moved reference from -inf gives alpha = 0.
+      const float a0 = need0 ? fast_exp2(m_run[0] - mx[0]) : 1.f;
+      const float a1 = need1 ? fast_exp2(m_run[1] - mx[1]) : 1.f;
+      const float mn0 = need0 ? mx[0] : m_run[0];
+      const float mn1 = need1 ? mx[1] : m_run[1];
+      l_run[0] *= a0;
+      l_run[1] *= a1;
 #pragma unroll
-        for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] *= alpha;
-        m_run[rt] = m_new;
+      for (int dt = 0; dt < DTILES; ++dt) {
+        o[0][dt] *= a0;
+        o[1][dt] *= a1;
       }
+      m_run[0] = mn0;
+      m_run[1] = mn1;
+    }
+    bf16x8 pb[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
       const float m_use = (m_run[rt] == kNegInf) ? 0.f : m_run[rt];
       float p[8];
       float psum = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        p[j] = fast_exp2(fmaf(x[j], scale_log2, -m_use));
+        p[j] = fast_exp2(fmaf(x[rt][j], scale_log2, -m_use));
         psum += p[j];
       }
       l_run[rt] += psum;
@@ -252,24 +316,12 @@ struct TileEngine {
                              pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])));
     }
 
-    // O^T += V^T P^T.  Lane (lg, l16) supplies V[token][dt*16 + 4*(l16%4)..+3]
+    // O^T += V^T P^T.  Lane (lg, l16) supplied V[token][dt*16 + 4*(l16%4)..+3]
     // of tokens lg*4 + l16/4 (first read) and 16 + lg*4 + l16/4 (second read)
-    // and receives V[tokens][dt*16 + l16], the A fragment rows of the MFMA.
-    const int r = l16 >> 2;
-    const int q4 = l16 & 3;
-    const int t0 = lg * 4 + r;
-    const int t1 = 16 + lg * 4 + r;
-    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    // and received V[tokens][dt*16 + l16], the A fragment rows of the MFMA.
 #pragma unroll
     for (int dt = 0; dt < DTILES; ++dt) {
-      const int dim = dt * 16 + 4 * q4;
-      const int c = dim >> 3;
-      const int boff = (dim & 7) * 2;
-      const uint8_t* p0 = vb + t0 * T::ROWB + T::v_slot(t0, c) * 16 + boff;
-      const uint8_t* p1 = vb + t1 * T::ROWB + T::v_slot(t1, c) * 16 + boff;
-      const bf16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((AIOS_LDS bf16x4*)(p0));
-      const bf16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((AIOS_LDS bf16x4*)(p1));
-      const bf16x8 vf = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+      const bf16x8 vf = __builtin_shufflevector(va[dt][0], va[dt][1], 0, 1, 2, 3, 4, 5, 6, 7);
       o[0][dt] = mfma16x16x32(vf, pb[0], o[0][dt]);
       o[1][dt] = mfma16x16x32(vf, pb[1], o[1][dt]);
     }

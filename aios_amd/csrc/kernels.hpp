@@ -8,11 +8,11 @@ namespace aios {
 
 // Partial softmax states of a decode batch live in one workspace array,
 // contiguous per (row b, kv-head h):
-//   parts_o  [B][Hkv][n_parts][G][D] fp32 (normalised o = acc / l)
+//   parts_o  [B][Hkv][n_parts][G][D] bf16 (normalised o = acc / l)
 //   parts_lse[B][Hkv][n_parts][G]    fp32 (log2-domain m + log2 l; -inf = empty)
 // Slot j < n_chunks holds prefix chunk j; slot n_chunks + s holds suffix split s.
 struct PartsArgs {
-  float* o;
+  bf16* o;
   float* lse;
   int32_t n_parts;
   int32_t n_chunks;
@@ -75,9 +75,15 @@ hipError_t build_indices(const int32_t* page_table, int64_t pt_stride, const int
                          const int32_t* cu_k, int32_t batch, int32_t max_len,
                          int32_t* indices, hipStream_t stream);
 
+// KV positions each 16-lane DPP row of a suffix wavefront holds per pass
+// (4 * tpg positions per pass), sized so the K/V slices fit the registers.
+__host__ __device__ constexpr int suffix_tpg(int D, int G) {
+  return G * D <= 384 ? 16 : (G * D <= 512 ? 8 : 4);
+}
+
 // One launch: prefix-chunk workgroups (MFMA tile engine) followed by suffix
-// workgroups (four (row, head, split) items per workgroup).
-hipError_t launch_decode_main(int D, int tpg, const DecodeArgs& a, hipStream_t stream);
+// workgroups (eight (row, head, split) items per workgroup).
+hipError_t launch_decode_main(int D, const DecodeArgs& a, hipStream_t stream);
 
 // Log-sum-exp merge of every part of each (row, kv-head) into bf16 out.
 hipError_t launch_decode_combine(int D, const DecodeArgs& a, hipStream_t stream);

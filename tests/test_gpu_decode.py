@@ -166,11 +166,12 @@ def test_long_rows_without_shared_prefix():
     np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
 
 
-@pytest.mark.parametrize("max_suffix", [33, 64, 65])
+@pytest.mark.parametrize("max_suffix", [33, 64, 65, 128, 129, 200])
 def test_single_launch_row_lengths(max_suffix):
-    # Rows of up to 64 positions are covered by one suffix item (16 per DPP row).
-    shape = DecodeShape("rows", 1, 6, 0, max_suffix, 8, 2, 96, 512, min_suffix=max_suffix)
+    # Rows of up to two passes of one suffix wavefront are covered by one item
+    # (no partials, no combine); longer rows are split and merged.
+    shape = DecodeShape("rows", 1, 6, 0, max_suffix, 8, 2, 96, 2048, min_suffix=max_suffix)
     wl = make_decode_workload(shape, seed=max_suffix)
     out, p = _run(wl, shared=0)
-    assert (p.num_parts == 1) == (max_suffix <= 64)
+    assert (p.num_parts == 1) == (max_suffix <= 2 * 4 * p.suffix_tpg)
     np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
