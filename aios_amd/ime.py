@@ -1,0 +1,343 @@
+"""CandidateGroup engine: one shared-prefix prefill, then N candidate
+continuations decoded as one batch over shared prefix KV pages.
+
+Restates the GPU control flow of ImeCompletionEngine (python/aios/ime.py):
+  * token-LCP prefix reuse across keystrokes with the strict-backspace rule
+    and persisted prefix pages/logits (_prepare_prefix, :1116-1168);
+  * prefix prefill or LCP extension prefill (:1170-1217);
+  * every candidate row of the page table starts with the same physical
+    prefix pages (:1155), so the backend reads them once per kv-head
+    (Batch.shared_prefix_len);
+  * the branch decode loop (:891-1114) with one freshly allocated page per
+    active row per step (:1219-1251), EOS compaction of active rows, and the
+    suffix pages freed when the group is done (:588-592), so the pages in
+    use after complete() equal the prefix length (tests/test_ime_gpu.py:36);
+  * KV budget check (:467-478) and latest-wins cancellation observed once per
+    decode step (:174-184, :971-973).
+Text governance and sampling are not restated (no tokenizer ships with the
+synthetic models): candidate i starts from the i-th most likely first token
+and then decodes greedily; candidates are ranked by average raw log-prob
+(the reference's base score before text penalties, :1109-1115).
+"""
+from __future__ import annotations
+
+import threading
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from aios_amd.config import ModelConfig
+from aios_amd.core import Batch, Context, Req, SamplingParams, reset_global_ctx, set_global_ctx
+from aios_amd.kvcache import MHAKVCache
+from aios_amd.qwen3 import Qwen3ForCausalLM
+from aios_amd.scheduler import CacheManager
+
+
+def token_longest_common_prefix(left, right) -> int:
+    """ime.py:165-171."""
+    n = 0
+    for a, b in zip(left, right):
+        if a != b:
+            break
+        n += 1
+    return n
+
+
+class CancellationToken:
+    """Latest-wins cancellation flag (ime.py:174-184)."""
+
+    def __init__(self, generation_id: int) -> None:
+        self.generation_id = generation_id
+        self._event = threading.Event()
+
+    def cancel(self) -> None:
+        self._event.set()
+
+    @property
+    def cancelled(self) -> bool:
+        return self._event.is_set()
+
+
+@dataclass(frozen=True)
+class CandidateGroupConfig:
+    num_candidates: int = 8
+    max_new_tokens: int = 16
+    display_candidates: int = 3
+    eos_token_id: int | None = None
+
+    def validate(self) -> None:
+        if self.num_candidates < self.display_candidates or self.display_candidates < 1:
+            raise ValueError("num_candidates must cover display_candidates")
+        if self.max_new_tokens < 1:
+            raise ValueError("max_new_tokens must be positive")
+
+
+@dataclass(frozen=True)
+class Candidate:
+    token_ids: tuple[int, ...]
+    average_logprob: float
+    stop_reason: str
+
+
+@dataclass
+class CompletionResult:
+    candidates: tuple[Candidate, ...]
+    raw_candidates: tuple[Candidate, ...]
+    prefix_tokens: int
+    reused_prefix_tokens: int
+    generated_tokens: int
+    active_model_tokens: int
+    latency_ms: float
+    gpu_latency_ms: float
+    unique_kv_pages: int
+    cancelled: bool
+    prefix_logits: torch.Tensor | None = field(default=None, repr=False)
+
+
+def select_top(candidates, k: int) -> tuple[Candidate, ...]:
+    """Highest average log-prob first, distinct token sequences only."""
+    seen = set()
+    out = []
+    for c in sorted(candidates, key=lambda c: c.average_logprob, reverse=True):
+        if c.token_ids in seen:
+            continue
+        seen.add(c.token_ids)
+        out.append(c)
+        if len(out) == k:
+            break
+    return tuple(out)
+
+
+class CandidateGroupRuntime:
+    """Model + paged KV pool + page allocator + global context on one GPU
+    (the parts of python/aios/llm/llm.py:27-96 the IME path uses)."""
+
+    def __init__(self, config: ModelConfig, weights: dict, device="cuda", num_pages: int = 4096,
+                 max_attempts: int = 8, workspace_size: int = 8 << 20) -> None:
+        from aios_amd.attention import Mi355xAttentionBackend
+
+        self.config = config
+        self.device = torch.device(device)
+        self.num_pages = num_pages
+        self.max_attempts = max_attempts
+        backend = Mi355xAttentionBackend(config, workspace_size=workspace_size)
+        self.model = Qwen3ForCausalLM(config, weights, self.device, attn_backend=backend)
+        self.kv_cache = MHAKVCache(config.num_kv_heads, config.num_layers, config.head_dim,
+                                   num_pages, 1, torch.bfloat16, self.device)
+        self.cache_manager = CacheManager(self.device, num_pages)
+        reset_global_ctx()
+        self.ctx = Context(page_size=1)
+        self.ctx.kv_cache = self.kv_cache
+        self.ctx.attn_backend = backend
+        set_global_ctx(self.ctx)
+
+
+class CandidateGroupEngine:
+    def __init__(self, rt: CandidateGroupRuntime) -> None:
+        self.rt = rt
+        self._generation_id = 0
+        self._active: CancellationToken | None = None
+        self._gen_lock = threading.Lock()
+        self._run_lock = threading.Lock()
+        self._prefix_ids: list[int] = []
+        self._prefix_pages: torch.Tensor | None = None
+        self._prefix_logits: torch.Tensor | None = None
+
+    # -- lifecycle -------------------------------------------------------------
+    def new_generation(self) -> CancellationToken:
+        with self._gen_lock:
+            if self._active is not None:
+                self._active.cancel()
+            self._generation_id += 1
+            self._active = CancellationToken(self._generation_id)
+            return self._active
+
+    def reset_prefix_cache(self) -> None:
+        with self._run_lock:
+            if self._prefix_pages is not None and len(self._prefix_pages):
+                self.rt.cache_manager._free(self._prefix_pages)
+            self._prefix_ids = []
+            self._prefix_pages = None
+            self._prefix_logits = None
+
+    # -- one keystroke ---------------------------------------------------------
+    @torch.inference_mode()
+    def complete(self, token_ids, config: CandidateGroupConfig | None = None,
+                 cancellation: CancellationToken | None = None) -> CompletionResult:
+        cancellation = cancellation or self.new_generation()
+        with self._run_lock:
+            return self._complete_locked(list(token_ids), config or CandidateGroupConfig(),
+                                         cancellation)
+
+    def _complete_locked(self, token_ids, config, cancellation) -> CompletionResult:
+        wall = time.perf_counter()
+        config.validate()
+        if not token_ids:
+            raise ValueError("prefix produced no input tokens")
+        n = config.num_candidates
+        if n > self.rt.max_attempts:
+            raise ValueError("num_candidates exceeds the page-table rows")
+        if cancellation.cancelled:
+            return CompletionResult((), (), len(token_ids), 0, 0, 0,
+                                    (time.perf_counter() - wall) * 1e3, 0.0, 0, True)
+        p = len(token_ids)
+        max_total = p + config.max_new_tokens
+        if max_total > self.rt.config.max_position_embeddings:
+            raise ValueError("prefix + output exceeds context limit")
+        required = p + n * max(0, config.max_new_tokens - 1)
+        if required > self.rt.num_pages:
+            raise ValueError(
+                f"CandidateGroup KV budget is too small: need up to {required} pages, "
+                f"configured {self.rt.num_pages}")
+        dev = self.rt.device
+        page_table = torch.zeros((self.rt.max_attempts, max_total), dtype=torch.int32, device=dev)
+        self.rt.ctx.page_table = page_table
+        started = torch.cuda.Event(enable_timing=True)
+        ended = torch.cuda.Event(enable_timing=True)
+        started.record()
+        allocated: list[torch.Tensor] = []
+        try:
+            prefix_logits, prefix_pages, reused = self._prepare_prefix(token_ids, page_table)
+            raw, allocated, generated, active_tokens, cancelled = self._generate(
+                prefix_logits, page_table, p, config, cancellation)
+            unique_pages = len(prefix_pages) + sum(len(a) for a in allocated)
+            if allocated:
+                self.rt.cache_manager._free(torch.cat(allocated))
+                allocated = []
+            ended.record()
+            ended.synchronize()
+            return CompletionResult(
+                candidates=select_top(raw, config.display_candidates),
+                raw_candidates=tuple(raw),
+                prefix_tokens=p,
+                reused_prefix_tokens=reused,
+                generated_tokens=generated,
+                active_model_tokens=active_tokens + (p - reused),
+                latency_ms=(time.perf_counter() - wall) * 1e3,
+                gpu_latency_ms=started.elapsed_time(ended),
+                unique_kv_pages=unique_pages,
+                cancelled=cancelled,
+                prefix_logits=prefix_logits,
+            )
+        finally:
+            if allocated:
+                self.rt.cache_manager._free(torch.cat(allocated))
+
+    # -- prefix ------------------------------------------------------------------
+    def _prepare_prefix(self, token_ids, page_table):
+        """Token-LCP reuse of the persisted prefix (ime.py:1116-1168)."""
+        old_ids, old_pages = self._prefix_ids, self._prefix_pages
+        reused = token_longest_common_prefix(old_ids, token_ids)
+        if old_pages is not None and self._prefix_logits is not None and \
+                reused == len(old_ids) == len(token_ids):
+            page_table[:, : len(token_ids)] = old_pages.unsqueeze(0)
+            return self._prefix_logits, old_pages, reused
+        if old_ids and reused == len(token_ids) < len(old_ids):
+            reused = 0  # strict backspace: re-prefill for exact final logits
+        if old_pages is not None:
+            kept = old_pages[:reused]
+            released = old_pages[reused:]
+            if len(released):
+                self.rt.cache_manager._free(released)
+        else:
+            kept = torch.empty(0, dtype=torch.int32, device=self.rt.device)
+        ext = self.rt.cache_manager.allocate(len(token_ids) - reused)
+        prefix_pages = torch.cat([kept, ext])
+        page_table[:, : len(token_ids)] = prefix_pages.unsqueeze(0)
+        logits = self._prefill(token_ids, reused, ext)
+        self._prefix_ids = list(token_ids)
+        self._prefix_pages = prefix_pages
+        self._prefix_logits = logits
+        return logits, prefix_pages, reused
+
+    def _prefill(self, token_ids, cached_len: int, out_pages: torch.Tensor) -> torch.Tensor:
+        """Prefix prefill (cached_len 0) or LCP extension (ime.py:1170-1217)."""
+        dev = self.rt.device
+        req = Req(input_ids=torch.empty(len(token_ids), dtype=torch.long), cached_len=cached_len,
+                  output_len=1, uid=0, sampling_params=SamplingParams(max_tokens=1), table_idx=0)
+        batch = Batch(reqs=[req], phase="prefill")
+        batch.input_ids = torch.tensor(token_ids[cached_len:], dtype=torch.long, device=dev)
+        batch.positions = torch.arange(cached_len, len(token_ids), dtype=torch.int32, device=dev)
+        batch.out_loc = out_pages
+        self.rt.model.attn_backend.prepare_metadata(batch)
+        with self.rt.ctx.forward_batch(batch):
+            return self.rt.model.forward()
+
+    # -- candidates --------------------------------------------------------------
+    def _decode_step(self, tokens: torch.Tensor, page_table, cached_len: int, rows: list[int],
+                     prefix_len: int):
+        """One decode forward over the active rows (ime.py:1219-1251)."""
+        dev = self.rt.device
+        pages = self.rt.cache_manager.allocate(len(rows))
+        row_t = torch.tensor(rows, dtype=torch.long, device=dev)
+        page_table[row_t, cached_len] = pages
+        reqs = [Req(input_ids=torch.empty(cached_len + 1, dtype=torch.long), cached_len=cached_len,
+                    output_len=1, uid=r, sampling_params=SamplingParams(max_tokens=1), table_idx=r)
+                for r in rows]
+        batch = Batch(reqs=reqs, phase="decode")
+        batch.input_ids = tokens
+        batch.positions = torch.full((len(rows),), cached_len, dtype=torch.int32, device=dev)
+        batch.out_loc = pages
+        batch.shared_prefix_len = prefix_len
+        self.rt.model.attn_backend.prepare_metadata(batch)
+        with self.rt.ctx.forward_batch(batch):
+            logits = self.rt.model.forward()
+        return logits, pages
+
+    def _generate(self, prefix_logits, page_table, prefix_len: int, config, cancellation):
+        n = config.num_candidates
+        dev = self.rt.device
+        t_max = config.max_new_tokens
+        out_ids = torch.full((n, t_max), -1, dtype=torch.long, device=dev)
+        logp_sum = torch.zeros(n, dtype=torch.float32, device=dev)
+        counts = torch.zeros(n, dtype=torch.long, device=dev)
+        eos_hit = torch.zeros(n, dtype=torch.bool, device=dev)
+        # First token of candidate i: the i-th most likely continuation.
+        lp0 = torch.log_softmax(prefix_logits[0].float(), dim=-1)
+        top = torch.topk(lp0, n)
+        token = top.indices
+        raw_lp = top.values
+        active = list(range(n))
+        allocated = []
+        cancelled = False
+        active_tokens = 0
+        for step in range(t_max):
+            if cancellation.cancelled:  # observed between steps (ime.py:971-973)
+                cancelled = True
+                break
+            if step:
+                lp = torch.log_softmax(logits.float(), dim=-1)
+                token = lp.argmax(dim=-1)
+                raw_lp = lp.gather(1, token[:, None]).squeeze(1)
+            act = torch.tensor(active, dtype=torch.long, device=dev)
+            emitted = torch.ones_like(token, dtype=torch.bool)
+            if config.eos_token_id is not None:
+                emitted = token.ne(config.eos_token_id)
+            out_ids[act, step] = torch.where(emitted, token, torch.full_like(token, -1))
+            logp_sum[act] += torch.where(emitted, raw_lp, torch.zeros_like(raw_lp))
+            counts[act] += emitted.long()
+            eos_hit[act] |= ~emitted
+            if step + 1 == t_max:
+                break
+            if config.eos_token_id is not None:
+                keep = emitted.cpu().tolist()  # row compaction (ime.py:1040-1046)
+                active = [r for r, k in zip(active, keep) if k]
+                token = token[emitted]
+                if not active:
+                    break
+            active_tokens += len(active)
+            logits, pages = self._decode_step(token, page_table, prefix_len + step, active,
+                                              prefix_len)
+            allocated.append(pages)
+        out_cpu = out_ids.cpu()
+        cnt = counts.cpu().tolist()
+        sums = logp_sum.cpu().tolist()
+        eos = eos_hit.cpu().tolist()
+        raw = []
+        for i in range(n):
+            ids = tuple(int(x) for x in out_cpu[i, : cnt[i]].tolist())
+            avg = sums[i] / cnt[i] if cnt[i] else float("-inf")
+            stop = "eos" if eos[i] else ("cancelled" if cancelled else "max_new_tokens")
+            raw.append(Candidate(ids, avg, stop))
+        return raw, allocated, int(sum(cnt)), active_tokens, cancelled

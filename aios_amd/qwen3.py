@@ -1,0 +1,158 @@
+"""Qwen3 / MiniMind decoder in PyTorch-ROCm eager, the caller of the backend.
+
+Restates python/aios/models/qwen3.py:31-173 and the layer ops it uses
+(python/aios/layers/norm.py:10-40, activation.py:9-12, rotary.py:8-29,
+attention.py:6-16, embedding.py:13-41) without FlashInfer: RMSNorm and the
+fused residual-add RMSNorm compute in fp32 and store bf16, SiLU-and-mul and
+RoPE are plain torch ops.  Attention goes through the backend exactly as in
+the reference: ``backend.forward(q, k, v, kv_cache, layer_id, batch)`` once
+per layer with q/k/v as ``[tokens, heads, head_dim]`` (v a strided view into
+the fused qkv projection).
+
+Weights are synthetic (seeded N(0, 0.02), norm weights 1, tied embedding);
+no checkpoint is loaded.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from aios_amd.attention import BaseAttentionBackend, Mi355xAttentionBackend
+from aios_amd.config import ModelConfig
+from aios_amd.core import get_global_ctx
+
+
+def init_weights(config: ModelConfig, seed: int, device="cpu",
+                 dtype: torch.dtype = torch.bfloat16, std: float = 0.02) -> dict:
+    """Seeded synthetic weights.  Generated on ``device`` with a generator of
+    that device, so CPU-generated weights copied to the GPU match a CPU run."""
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    h, d = config.hidden_size, config.head_dim
+    q_size, kv_size = config.num_qo_heads * d, config.num_kv_heads * d
+
+    def lin(out_f, in_f):
+        return (torch.randn(out_f, in_f, generator=g, device=dev, dtype=torch.float32) * std).to(dtype)
+
+    w = {"embed": lin(config.vocab_size, h), "final_norm": torch.ones(h, device=dev, dtype=dtype),
+         "layers": []}
+    for _ in range(config.num_layers):
+        w["layers"].append({
+            "input_norm": torch.ones(h, device=dev, dtype=dtype),
+            "qkv": lin(q_size + 2 * kv_size, h),
+            "q_norm": torch.ones(d, device=dev, dtype=dtype),
+            "k_norm": torch.ones(d, device=dev, dtype=dtype),
+            "o": lin(h, q_size),
+            "post_norm": torch.ones(h, device=dev, dtype=dtype),
+            "gate_up": lin(2 * config.intermediate_size, h),
+            "down": lin(h, config.intermediate_size),
+        })
+    return w
+
+
+def weights_to(w: dict, device, dtype=None) -> dict:
+    def mv(t):
+        t = t.to(device)
+        return t.to(dtype) if dtype is not None else t
+    return {"embed": mv(w["embed"]), "final_norm": mv(w["final_norm"]),
+            "layers": [{k: mv(v) for k, v in lw.items()} for lw in w["layers"]]}
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """fp32 RMSNorm, stored in the input dtype (norm.py:18-22)."""
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * weight.float()
+    return y.to(x.dtype)
+
+
+def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                      eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """residual <- x + residual; x <- RMSNorm(residual) (norm.py:34-40)."""
+    r = x.float() + residual.float()
+    y = r * torch.rsqrt(r.pow(2).mean(-1, keepdim=True) + eps) * weight.float()
+    return y.to(x.dtype), r.to(residual.dtype)
+
+
+def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    """silu(x[:, :I]) * x[:, I:] (activation.py:9-12)."""
+    gate, up = x.chunk(2, dim=-1)
+    return F.silu(gate) * up
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    x1, x2 = x.chunk(2, dim=-1)
+    return torch.cat((-x2, x1), dim=-1)
+
+
+class RotaryEmbedding:
+    """cos/sin cache (rotary.py:8-29)."""
+
+    def __init__(self, head_dim: int, max_positions: int, base: float, device) -> None:
+        inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+        t = torch.arange(max_positions, dtype=torch.float32)
+        emb = torch.cat((torch.outer(t, inv_freq),) * 2, dim=-1)
+        self.cos = emb.cos().to(device)
+        self.sin = emb.sin().to(device)
+
+    def __call__(self, positions: torch.Tensor):
+        idx = positions.long()
+        return self.cos[idx].unsqueeze(1), self.sin[idx].unsqueeze(1)
+
+
+def apply_rotary_pos_emb(q, k, cos, sin):
+    """attention.py:11-16 (cos/sin cast to the activation dtype)."""
+    cos = cos.to(q.dtype)
+    sin = sin.to(q.dtype)
+    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+
+class Qwen3ForCausalLM:
+    """Decoder + tied LM head.  ``forward()`` reads the batch from the global
+    context like the reference (qwen3.py:140-173)."""
+
+    def __init__(self, config: ModelConfig, weights: dict, device,
+                 attn_backend: BaseAttentionBackend | None = None,
+                 max_positions: int | None = None) -> None:
+        self.config = config
+        self.device = torch.device(device)
+        self.w = weights
+        self.attn_backend = attn_backend or Mi355xAttentionBackend(config)
+        self.rotary = RotaryEmbedding(config.head_dim,
+                                      max_positions or min(config.max_position_embeddings, 8192),
+                                      config.rope_theta, self.device)
+        self._q_size = config.num_qo_heads * config.head_dim
+        self._kv_size = config.num_kv_heads * config.head_dim
+
+    def _attention(self, i: int, h: torch.Tensor, cos, sin, kv_cache, batch) -> torch.Tensor:
+        c = self.config
+        lw = self.w["layers"][i]
+        t = h.shape[0]
+        qkv = F.linear(h, lw["qkv"])
+        q, k, v = qkv.split([self._q_size, self._kv_size, self._kv_size], dim=-1)
+        q = rmsnorm(q.reshape(t, c.num_qo_heads, c.head_dim), lw["q_norm"], c.rms_norm_eps)
+        k = rmsnorm(k.reshape(t, c.num_kv_heads, c.head_dim), lw["k_norm"], c.rms_norm_eps)
+        v = v.view(t, c.num_kv_heads, c.head_dim)
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        out = self.attn_backend.forward(q.contiguous(), k.contiguous(), v, kv_cache, i, batch)
+        return F.linear(out.reshape(t, -1), lw["o"])
+
+    def forward(self) -> torch.Tensor:
+        ctx = get_global_ctx()
+        batch = ctx.batch
+        c = self.config
+        h = F.embedding(batch.input_ids, self.w["embed"])
+        cos, sin = self.rotary(batch.positions)
+        residual = None
+        for i, lw in enumerate(self.w["layers"]):
+            if residual is None:
+                residual = h
+                x = rmsnorm(h, lw["input_norm"], c.rms_norm_eps)
+            else:
+                x, residual = fused_add_rmsnorm(h, residual, lw["input_norm"], c.rms_norm_eps)
+            x = self._attention(i, x, cos, sin, ctx.kv_cache, batch)
+            x, residual = fused_add_rmsnorm(x, residual, lw["post_norm"], c.rms_norm_eps)
+            h = F.linear(silu_and_mul(F.linear(x, lw["gate_up"])), lw["down"])
+        x, _ = fused_add_rmsnorm(h, residual, self.w["final_norm"], c.rms_norm_eps)
+        if batch.is_prefill and not batch.return_all_logits:
+            x = x[batch.attn_metadata.get_last_indices(batch.size)]
+        return F.linear(x, self.w["embed"])

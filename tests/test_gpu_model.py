@@ -1,0 +1,244 @@
+"""Full-model parity: the CandidateGroup engine on the gfx950 backend vs the
+float32 CPU oracle model (oracle/model.py) with the same seeded bf16 weights.
+
+Acceptance follows the reference's backend equivalence check
+(scripts/check_attnres_runtime_equivalence.py:37-47, 82-89, 234-251):
+full-vocabulary logit max-abs within LOGIT_TOL, Top-1 / Top-3 token-id sets
+of the logits equal (topk overlap at k in {1, 3}), identical discrete
+decisions, and average log-probs within AVG_LP_TOL.  Synthetic N(0, 0.02)
+weights give nearly flat next-token distributions (top-1/top-2 log-prob gaps
+of a few 1e-3 occur in every 16-step run), while bf16 GPU logits differ from
+float32 ones by about 0.03; so set equality is asserted wherever the oracle's
+own margin exceeds SET_MARGIN = 2 * LOGIT_TOL_TIGHT (below that, either order is
+a valid bf16 outcome), and every discrete GPU decision must be the oracle's
+choice up to a gap of 2 * (observed logit deviation at that step).
+"""
+from __future__ import annotations
+
+from dataclasses import replace
+
+import pytest
+import torch
+
+from aios_amd.config import MINIMIND_0P1B, MINIMIND_IME_0P1B, QWEN3_0P6B
+from aios_amd.core import reset_global_ctx
+from aios_amd.ime import CancellationToken, CandidateGroupConfig, CandidateGroupEngine, CandidateGroupRuntime
+from aios_amd.qwen3 import init_weights, weights_to
+from oracle.model import OracleModel, top3_by_average
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 0.125        # reference equivalence-check default (bf16 full-vocab logits)
+LOGIT_TOL_TIGHT = 0.05   # what this build holds itself to (measured ~0.03)
+SET_MARGIN = 2 * LOGIT_TOL_TIGHT
+AVG_LP_TOL = 0.02
+# Seeds whose prefix logits have top-1 and top-3 margins above SET_MARGIN
+# in the oracle (MiniMind-0.1B shape, 32-token prefix).
+SCREENED_SEEDS = (4, 15, 22)
+
+
+def _prefix(seed: int, n: int, vocab: int) -> list[int]:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(vocab, (n,), generator=g).tolist()
+
+
+def _engine(config, seed, num_pages=1024):
+    w = init_weights(config, seed, "cpu")
+    rt = CandidateGroupRuntime(config, weights_to(w, "cuda"), "cuda", num_pages=num_pages)
+    return CandidateGroupEngine(rt), OracleModel(config, w)
+
+
+def _record_decode_logits(eng):
+    """Wrap the decode step to keep each step's logits and active rows."""
+    steps = []
+    inner = eng._decode_step
+
+    def wrapped(tokens, page_table, cached_len, rows, prefix_len):
+        logits, pages = inner(tokens, page_table, cached_len, rows, prefix_len)
+        steps.append((list(rows), logits.float().cpu()))
+        return logits, pages
+
+    eng._decode_step = wrapped
+    return steps
+
+
+def _set_equal_if_screened(gpu: torch.Tensor, ref: torch.Tensor, k: int) -> bool | None:
+    """Top-k id sets must match when the oracle's k-th/k+1-th gap clears SET_MARGIN."""
+    s = ref.sort(descending=True).values
+    if (s[k - 1] - s[k]).item() <= SET_MARGIN:
+        return None
+    return set(gpu.topk(k).indices.tolist()) == set(ref.topk(k).indices.tolist())
+
+
+def teardown_function(_):
+    reset_global_ctx()
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("seed", SCREENED_SEEDS)
+def test_prefix_logits_and_top_sets(seed):
+    c = MINIMIND_0P1B
+    eng, om = _engine(c, seed)
+    prefix = _prefix(seed, 32, c.vocab_size)
+    res = eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=1))
+    gpu = res.prefix_logits[0].float().cpu()
+    ref = om.logits(torch.tensor(prefix)[None], 31)[0, -1]
+    diff = (gpu - ref).abs().max().item()
+    assert diff <= LOGIT_TOL_TIGHT <= LOGIT_TOL, diff
+    assert torch.nn.functional.cosine_similarity(gpu, ref, dim=0).item() > 0.999
+    assert _set_equal_if_screened(gpu, ref, 1) is True
+    assert _set_equal_if_screened(gpu, ref, 3) is True
+
+
+@pytest.mark.parametrize("config", [MINIMIND_IME_0P1B.with_layers(4),
+                                    replace(QWEN3_0P6B, num_layers=4, vocab_size=8192)],
+                         ids=["minimind-ime-h64-g3", "qwen3-0.6b-h128-g2"])
+def test_prefix_logits_other_shapes(config):
+    eng, om = _engine(config, 3)
+    prefix = _prefix(3, 48, config.vocab_size)
+    res = eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=1))
+    gpu = res.prefix_logits[0].float().cpu()
+    ref = om.logits(torch.tensor(prefix)[None], 47)[0, -1]
+    assert (gpu - ref).abs().max().item() <= LOGIT_TOL_TIGHT
+
+
+def _check_candidate_group(eng, om, prefix, n, steps):
+    rec = _record_decode_logits(eng)
+    res = eng.complete(prefix, CandidateGroupConfig(num_candidates=n, max_new_tokens=steps))
+    assert not res.cancelled and len(res.raw_candidates) == n
+    ids = torch.tensor([c.token_ids for c in res.raw_candidates])
+    assert ids.shape == (n, steps)
+    tf = om.teacher_forced(prefix, ids)  # oracle log-probs on the GPU's own histories
+    # step 0: candidate i takes the i-th best first token
+    ref0 = tf[0, 0]
+    top_vals = ref0.sort(descending=True).values[:n]
+    d0 = (res.prefix_logits[0].float().cpu().log_softmax(-1) - ref0).abs().max().item()
+    assert d0 <= LOGIT_TOL_TIGHT
+    chosen0 = ref0[ids[:, 0]]
+    assert (chosen0 - top_vals).abs().max().item() <= 2 * d0 + 1e-6
+    assert len(rec) == steps - 1
+    checked_sets = 0
+    for j, (rows, logits) in enumerate(rec, start=1):
+        assert rows == list(range(n))
+        ref = tf[:, j]
+        gpu_lp = logits.log_softmax(-1)
+        dev = (gpu_lp - ref).abs().max().item()
+        assert dev <= LOGIT_TOL_TIGHT, (j, dev)
+        tok = ids[:, j]
+        assert torch.equal(tok, gpu_lp.argmax(-1))  # greedy on the GPU's logits
+        gap = ref.max(-1).values - ref.gather(1, tok[:, None]).squeeze(1)
+        assert gap.max().item() <= 2 * dev + 1e-6, (j, gap)
+        for r in range(n):
+            for k in (1, 3):
+                ok = _set_equal_if_screened(logits[r], ref[r], k)
+                if ok is not None:
+                    assert ok, (j, r, k)
+                    checked_sets += 1
+    assert checked_sets >= n * (steps - 1) // 2  # most positions are screened in
+    avg_ref = tf.gather(2, ids[:, :, None]).squeeze(2).mean(1)
+    avg_gpu = torch.tensor([c.average_logprob for c in res.raw_candidates])
+    assert (avg_ref - avg_gpu).abs().max().item() <= AVG_LP_TOL
+    # Top-3 by average log-prob: the oracle's ranking of the same sequences
+    # agrees wherever neighbouring averages are apart by more than AVG_LP_TOL.
+    top_gpu = top3_by_average(ids, avg_gpu)
+    assert [c.token_ids for c in res.candidates] == top_gpu
+    order = torch.argsort(avg_ref, descending=True)
+    a = avg_ref[order]
+    if (a[2] - a[3]).item() > 2 * AVG_LP_TOL:
+        assert set(top3_by_average(ids, avg_ref)) == set(top_gpu)
+    if (a[0] - a[1]).item() > 2 * AVG_LP_TOL:
+        assert top3_by_average(ids, avg_ref)[0] == top_gpu[0]
+    return res
+
+
+def test_candidate_group_minimind_0p1b():
+    """Prefill a 32-token prefix, 8 candidates x 16 greedy steps over shared prefix KV."""
+    c = MINIMIND_0P1B
+    eng, om = _engine(c, 20260814)
+    _check_candidate_group(eng, om, _prefix(20260814, 32, c.vocab_size), 8, 16)
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages - 32
+    eng.reset_prefix_cache()
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages
+
+
+def test_candidate_group_long_prefix_cascade():
+    """Prefix >= 128 tokens: the decode plan uses the shared-prefix cascade."""
+    c = replace(QWEN3_0P6B, num_layers=3, vocab_size=8192)
+    eng, om = _engine(c, 11)
+    prefix = _prefix(11, 200, c.vocab_size)
+    plans = []
+    inner = eng.rt.model.attn_backend.prepare_metadata
+
+    def spy(batch):
+        md = inner(batch)
+        plans.append((batch.phase, md.plan.num_prefix_chunks, md.plan.prefix_len))
+        return md
+
+    eng.rt.model.attn_backend.prepare_metadata = spy
+    _check_candidate_group(eng, om, prefix, 8, 6)
+    decode_plans = [p for p in plans if p[0] == "decode"]
+    assert decode_plans and all(p[2] == 200 and p[1] >= 1 for p in decode_plans)
+
+
+def test_lcp_extension_and_strict_backspace():
+    """Cross-keystroke reuse: +2 tokens prefills only the extension against the
+    cached prefix; deleting back to the old prefix re-prefills from scratch."""
+    c = replace(QWEN3_0P6B, num_layers=4, vocab_size=8192)
+    eng, om = _engine(c, 5)
+    base = _prefix(5, 128, c.vocab_size)
+    ext = base + _prefix(6, 2, c.vocab_size)
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=4)
+    r0 = eng.complete(base, cfg)
+    assert r0.reused_prefix_tokens == 0
+    r1 = eng.complete(ext, cfg)
+    assert r1.reused_prefix_tokens == 128 and r1.active_model_tokens == 2 + 8 * 3
+    ref = om.logits(torch.tensor(ext)[None], 129)[0, -1]
+    assert (r1.prefix_logits[0].float().cpu() - ref).abs().max().item() <= LOGIT_TOL_TIGHT
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages - 130
+    r2 = eng.complete(base, cfg)  # strict backspace
+    assert r2.reused_prefix_tokens == 0
+    ref = om.logits(torch.tensor(base)[None], 127)[0, -1]
+    assert (r2.prefix_logits[0].float().cpu() - ref).abs().max().item() <= LOGIT_TOL_TIGHT
+    r3 = eng.complete(base, cfg)  # identical prefix: cached logits, no prefill
+    assert r3.reused_prefix_tokens == 128 and r3.active_model_tokens == 8 * 3
+    assert torch.equal(r3.prefix_logits, r2.prefix_logits)
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages - 128
+
+
+def test_cancelled_and_budget():
+    c = MINIMIND_0P1B.with_layers(2)
+    eng, _ = _engine(c, 1, num_pages=256)
+    tok = CancellationToken(1)
+    tok.cancel()
+    res = eng.complete(_prefix(1, 32, c.vocab_size), CandidateGroupConfig(), cancellation=tok)
+    assert res.cancelled and res.candidates == ()
+    assert eng.rt.cache_manager.available_size == 256
+    with pytest.raises(ValueError, match="KV budget"):
+        eng.complete(_prefix(1, 200, c.vocab_size), CandidateGroupConfig(max_new_tokens=16))
+    # a newer generation cancels the older one (latest wins)
+    t1 = eng.new_generation()
+    t2 = eng.new_generation()
+    assert t1.cancelled and not t2.cancelled
+
+
+def test_eos_compaction():
+    """Rows whose token is EOS stop; the rest keep decoding as a compacted batch."""
+    c = MINIMIND_0P1B.with_layers(4)
+    eng, om = _engine(c, 9)
+    prefix = _prefix(9, 32, c.vocab_size)
+    first = eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=6))
+    ids = [cand.token_ids for cand in first.raw_candidates]
+    eos = ids[2][0]  # candidate 2's first token becomes EOS
+    rec = _record_decode_logits(eng)
+    res = eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=6,
+                                                    eos_token_id=eos))
+    assert res.raw_candidates[2].token_ids == () and res.raw_candidates[2].stop_reason == "eos"
+    assert all(2 not in rows for rows, _ in rec)
+    for i, cand in enumerate(res.raw_candidates):
+        if i == 2 or not cand.token_ids:
+            continue
+        seq = torch.tensor([cand.token_ids])
+        tf = om.teacher_forced(prefix, seq)[0]
+        gap = tf.max(-1).values - tf.gather(1, seq[0][:, None]).squeeze(1)
+        assert gap[1:].max().item() <= 2 * LOGIT_TOL_TIGHT
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages - 32
