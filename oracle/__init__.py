@@ -36,9 +36,13 @@ Modules and what pins each function (the checks live in tests/test_oracle.py):
   model.py      float32 CPU restatement of the Qwen3 decoder and the greedy
                 CandidateGroup decode loop (models/qwen3.py:31-173,
                 layers/*.py, ime.py:891-1251) used for full-model Top-1/3
-                parity.  Its building blocks are pinned by closed forms
-                (RMSNorm of a constant row, RoPE at position 0 is identity,
-                RoPE preserves norms); the composition itself is
-                "parity unpinned" against the reference (no reference weights
-                or logits exist offline).
+                parity.  Pinned by closed forms (RoPE pair rotation by
+                pos * theta^(-2i/D), identity at position 0, norm
+                preservation; with every projection zeroed the logits are
+                RMSNorm(embed) @ embed^T) and by agreement with the product
+                decoder's fused residual-add composition run in float32 on
+                the CPU with the float64 attention above.  Against the
+                reference itself the composition is "parity unpinned": no
+                reference weights, logits or runnable FlashInfer exist
+                offline.
 """

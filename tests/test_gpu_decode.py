@@ -60,6 +60,25 @@ def test_op_test_config_cascade():
     np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
 
 
+def test_op_test_golden_fixture():
+    """HIP output on the committed op-test fixture's inputs vs its stored
+    float64 output (tests/golden/op_test_decode.npz)."""
+    import os
+
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "op_test_decode.npz"))
+    t = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(DEV)
+    n = len(fx["cu_k"]) - 1
+    cu_k = torch.from_numpy(fx["cu_k"])
+    for chunk in (0, 32):
+        p = paged.plan("decode", torch.arange(n + 1, dtype=torch.int32), cu_k, 8, 2, 96,
+                       shared_prefix_len=24, workspace_bytes=16 << 20, prefix_chunk_len=chunk)
+        ws = torch.empty(max(p.ws_bytes, 1), dtype=torch.uint8, device=DEV)
+        out = paged.decode(p, t(fx["q_bits"]), t(fx["k_bits"]), t(fx["v_bits"]),
+                           torch.from_numpy(fx["indices"]).to(DEV), cu_k.to(DEV), workspace=ws)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(to_np64(out), fx["out"], **BF16_TOL)
+
+
 def test_op_test_config_without_shared_prefix():
     wl = make_decode_workload(OP_TEST, seed=20260814)
     out, p = _run(wl, shared=0)

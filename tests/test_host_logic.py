@@ -1,0 +1,70 @@
+"""Host-side logic that needs no GPU: page allocator, LCP helper, candidate
+selection and the engine's argument checks (CPU only)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from aios_amd.core import Req, SamplingParams
+from aios_amd.ime import Candidate, CandidateGroupConfig, select_top, token_longest_common_prefix
+from aios_amd.scheduler import CacheManager
+from oracle import prefix as oprefix
+
+
+def test_cache_manager_order_is_deterministic():
+    """python/aios/scheduler/cache.py:9-51: first-free allocation, frees appended."""
+    cm = CacheManager(torch.device("cpu"), 10)
+    a = cm.allocate(3)
+    assert a.tolist() == [0, 1, 2] and cm.available_size == 7
+    b = cm.allocate(2)
+    assert b.tolist() == [3, 4]
+    cm._free(a[1:])
+    assert cm.available_size == 7
+    assert cm.allocate(6).tolist() == [5, 6, 7, 8, 9, 1]
+    assert cm.allocate(1).tolist() == [2]
+    with pytest.raises(NotImplementedError):
+        cm.allocate(1)
+
+
+def test_cache_manager_allocate_paged():
+    cm = CacheManager(torch.device("cpu"), 16)
+    table = torch.full((3, 8), -1, dtype=torch.int32)
+    reqs = [Req(input_ids=torch.zeros(5), cached_len=2, output_len=1, uid=0,
+                sampling_params=SamplingParams(), table_idx=2),
+            Req(input_ids=torch.zeros(3), cached_len=3, output_len=1, uid=1,
+                sampling_params=SamplingParams(), table_idx=0)]
+    cm.allocate_paged(reqs, table)
+    assert table[2].tolist() == [-1, -1, 0, 1, 2, -1, -1, -1]
+    assert table[0].tolist() == [-1] * 8  # extend_len 0: nothing allocated
+
+
+@pytest.mark.parametrize("old,new", [([1, 2, 3], [1, 2, 3]), ([1, 2], [1, 2, 3, 4]),
+                                     ([1, 2, 3, 4], [1, 2, 8]), ([5], [6]), ([], [1])])
+def test_lcp_matches_oracle(old, new):
+    assert token_longest_common_prefix(old, new) == oprefix.token_lcp(old, new)
+
+
+def test_select_top_distinct_by_average():
+    cands = [Candidate((1,), -1.0, "max_new_tokens"), Candidate((2,), -0.5, "max_new_tokens"),
+             Candidate((1,), -0.1, "max_new_tokens"), Candidate((3,), -2.0, "eos"),
+             Candidate((), float("-inf"), "eos")]
+    top = select_top(cands, 3)
+    assert [c.token_ids for c in top] == [(1,), (2,), (3,)]
+    assert top[0].average_logprob == -0.1
+
+
+def test_group_config_validation():
+    with pytest.raises(ValueError):
+        CandidateGroupConfig(num_candidates=2, display_candidates=3).validate()
+    with pytest.raises(ValueError):
+        CandidateGroupConfig(max_new_tokens=0).validate()
+    CandidateGroupConfig().validate()
+
+
+def test_req_lengths_follow_reference():
+    """core.py:27-59: extend_len = device_len - cached_len; complete_one advances."""
+    r = Req(input_ids=torch.zeros(7), cached_len=4, output_len=2, uid=0,
+            sampling_params=SamplingParams())
+    assert (r.device_len, r.extend_len, r.remain_len) == (7, 3, 2)
+    r.complete_one()
+    assert (r.cached_len, r.device_len, r.extend_len, r.remain_len) == (7, 8, 1, 1)

@@ -1,0 +1,398 @@
+"""Pins the CPU oracle before it is trusted as the checker (CPU only).
+
+Each oracle function is checked against something other than its own
+formula: the known answers the reference's resources hold (literal data
+below, with the file they come from), an independent library routine
+(numpy fancy-index assignment, torch's scaled_dot_product_attention), closed
+forms, and invariants chosen so that a dropped term, a wrong sign, a wrong
+head/page index or a transposed operand fails at least one of them.
+"""
+from __future__ import annotations
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from aios_amd.workloads import OP_TEST, make_decode_workload
+from oracle import attention as oatt
+from oracle import kv_store, metadata, prefix
+from oracle.model import OracleModel, _rope, top3_by_average
+from oracle.sdpa_cpu import paged_attention_cpu, sdpa_prefill_attention
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# --- paged KV scatter ---------------------------------------------------------
+
+def test_scatter_known_answer_lesson30():
+    """resources/lesson-30-triton-kv-store/run_lesson30.py:13-22: indices
+    [17, 4, 9], width 8, token t row = t*100 + offset, 20 rows of -1."""
+    width = 8
+    values = np.array([[t * 100 + o for o in range(width)] for t in range(3)], dtype=np.int64)
+    cache = np.full((20, width), -1, dtype=np.int64)
+    out = kv_store.scatter_rows(cache, np.array([17, 4, 9]), values)
+    assert out[17].tolist() == list(range(0, 8))
+    assert out[4].tolist() == list(range(100, 108))
+    assert out[9].tolist() == list(range(200, 208))
+    untouched = [r for r in range(20) if r not in (17, 4, 9)]
+    assert (out[untouched] == -1).all()
+    assert (cache == -1).all()  # input not modified
+
+
+def test_store_kv_matches_fancy_index_assignment():
+    rng = np.random.default_rng(0)
+    k_cache = rng.integers(0, 1 << 16, (64, 2, 96), dtype=np.uint16)
+    v_cache = rng.integers(0, 1 << 16, (64, 2, 96), dtype=np.uint16)
+    idx = rng.permutation(64)[:13].astype(np.int32)
+    k = rng.integers(0, 1 << 16, (13, 2, 96), dtype=np.uint16)
+    v = rng.integers(0, 1 << 16, (13, 2, 96), dtype=np.uint16)
+    ko, vo = kv_store.store_kv(k_cache, v_cache, idx, k, v)
+    ke, ve = k_cache.copy(), v_cache.copy()
+    ke[idx] = k
+    ve[idx] = v
+    assert np.array_equal(ko, ke) and np.array_equal(vo, ve)
+    assert not np.array_equal(ko, vo)  # K and V halves are not swapped
+
+
+@pytest.mark.parametrize("bad", ["cache_ndim", "layout", "count"])
+def test_store_kv_validation(bad):
+    kc = np.zeros((8, 2, 4), np.uint16)
+    k = np.zeros((3, 2, 4), np.uint16)
+    idx = np.arange(3)
+    if bad == "cache_ndim":
+        kc = kc.reshape(8, 8)
+    elif bad == "layout":
+        k = np.zeros((3, 4, 2), np.uint16)
+    else:
+        idx = np.arange(2)
+    with pytest.raises(ValueError):
+        kv_store.store_kv(kc, kc if kc.ndim == 3 else kc, idx, k, k)
+
+
+# --- metadata -----------------------------------------------------------------
+
+def test_metadata_known_answer_lesson26():
+    """resources/lesson-26-flashinfer-backend/run_lesson26.py:2-17."""
+    pages = [[7, 4, 9], [2, 8, 1, 6, 3]]
+    table = np.full((2, 5), -1, dtype=np.int32)
+    for r, p in enumerate(pages):
+        table[r, : len(p)] = p
+    md = metadata.build_metadata([3, 2], [3, 5], table, [0, 1])
+    assert md["cu_seqlens_q"].tolist() == [0, 3, 5]
+    assert md["cu_seqlens_k"].tolist() == [0, 3, 8]
+    assert md["indices"].tolist() == [7, 4, 9, 2, 8, 1, 6, 3]
+    assert md["last_indices"].tolist() == [2, 4]
+    assert md["last_page_len"].tolist() == [1, 1]
+
+
+def test_metadata_known_answer_lesson32_row_order():
+    """resources/lesson-32-flashinfer-paged-attention/run_lesson32.py:14-29,
+    with the requests stored in swapped page-table rows."""
+    table = np.full((4, 5), -1, dtype=np.int32)
+    table[3, :3] = [10, 11, 12]
+    table[1, :5] = [20, 21, 22, 23, 24]
+    md = metadata.build_metadata([3, 2], [3, 5], table, [3, 1])
+    assert md["cu_seqlens_q"].tolist() == [0, 3, 5]
+    assert md["cu_seqlens_k"].tolist() == [0, 3, 8]
+    assert md["indices"].tolist() == [10, 11, 12, 20, 21, 22, 23, 24]
+
+
+# --- attention ----------------------------------------------------------------
+
+def _offset_causal_sdpa(q, k, v, cached, scale):
+    """torch's SDPA with an explicit boolean mask (independent of the oracle)."""
+    g = q.shape[1] // k.shape[1]
+    qb = torch.from_numpy(q).double().transpose(0, 1)
+    kb = torch.from_numpy(k).double().transpose(0, 1).repeat_interleave(g, 0)
+    vb = torch.from_numpy(v).double().transpose(0, 1).repeat_interleave(g, 0)
+    qpos = torch.arange(cached, cached + q.shape[0])[:, None]
+    kpos = torch.arange(k.shape[0])[None, :]
+    out = F.scaled_dot_product_attention(qb, kb, vb, attn_mask=kpos <= qpos, scale=scale)
+    return out.transpose(0, 1).numpy()
+
+
+@pytest.mark.parametrize("cached", [0, 2])
+def test_reference_offset_causal_case_seed17(cached):
+    """tests/test_attention_backend.py:25-53 (seed 17, q_len 3, 4q/2kv, D=8)
+    against torch SDPA and the committed fixture."""
+    fx = np.load(os.path.join(GOLDEN, "offset_causal.npz"))
+    g = torch.Generator().manual_seed(17)
+    q = torch.randn(3, 4, 8, generator=g).numpy()
+    k = torch.randn(cached + 3, 2, 8, generator=g).numpy()
+    v = torch.randn(cached + 3, 2, 8, generator=g).numpy()
+    assert np.array_equal(q, fx[f"q{cached}"]) and np.array_equal(k, fx[f"k{cached}"])
+    out = oatt.attention_one(q, k, v, cached, 8 ** -0.5)
+    np.testing.assert_allclose(out, _offset_causal_sdpa(q, k, v, cached, 8 ** -0.5),
+                               rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(out, fx[f"out{cached}"], rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("shape", [(5, 8, 2, 96, 7), (1, 4, 4, 64, 0), (9, 12, 4, 128, 30)])
+def test_attention_matches_sdpa_random(shape):
+    lq, hq, hkv, d, cached = shape
+    rng = np.random.default_rng(lq * 1000 + d)
+    q = rng.standard_normal((lq, hq, d))
+    k = rng.standard_normal((cached + lq, hkv, d))
+    v = rng.standard_normal((cached + lq, hkv, d))
+    np.testing.assert_allclose(oatt.attention_one(q, k, v, cached, d ** -0.5),
+                               _offset_causal_sdpa(q, k, v, cached, d ** -0.5),
+                               rtol=1e-10, atol=1e-12)
+
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(3)
+    lq, hq, hkv, d = 4, 8, 2, 16
+    # Constant keys: uniform weights over the visible keys -> running means of v.
+    q = rng.standard_normal((lq, hq, d))
+    k = np.ones((lq, hkv, d))
+    v = rng.standard_normal((lq, hkv, d))
+    out = oatt.attention_one(q, k, v, 0, 0.25)
+    for i in range(lq):
+        means = v[: i + 1].mean(axis=0)  # [hkv, d]
+        np.testing.assert_allclose(out[i], np.repeat(means, hq // hkv, axis=0), atol=1e-12)
+    # First query with cached_len 0 sees only key 0 -> exactly v[0].
+    np.testing.assert_allclose(out[0], np.repeat(v[0], hq // hkv, axis=0), atol=1e-15)
+    # GQA mapping: query head h reads kv head h // G (not h % Hkv).
+    vv = np.zeros((2, hkv, d))
+    vv[:, 0] = 1.0
+    vv[:, 1] = 2.0
+    out = oatt.attention_one(rng.standard_normal((1, hq, d)), rng.standard_normal((2, hkv, d)),
+                             vv, 1, 1.0)
+    assert np.allclose(out[0, :4], 1.0) and np.allclose(out[0, 4:], 2.0)
+    # Two keys, scores a and b: weights are the logistic of (a - b) * scale.
+    qq = np.zeros((1, 1, 2))
+    qq[0, 0] = [1.0, 0.0]
+    kk = np.array([[[3.0, 0.0]], [[-1.0, 0.0]]])
+    vk = np.array([[[1.0, 0.0]], [[0.0, 1.0]]])
+    o = oatt.attention_one(qq, kk, vk, 1, 0.5)
+    w0 = 1.0 / (1.0 + math.exp(-(3.0 - -1.0) * 0.5))
+    np.testing.assert_allclose(o[0, 0], [w0, 1.0 - w0], atol=1e-15)
+
+
+def test_paged_attention_page_permutation_and_decode():
+    rng = np.random.default_rng(5)
+    hq, hkv, d, pages = 8, 2, 32, 40
+    kc = rng.standard_normal((pages, hkv, d))
+    vc = rng.standard_normal((pages, hkv, d))
+    kv_lens = [7, 1, 12]
+    perm = rng.permutation(pages)
+    idx = perm[: sum(kv_lens)].astype(np.int32)
+    cu_k = metadata.cumulative(kv_lens)
+    q = rng.standard_normal((3, hq, d))
+    out = oatt.decode_attention(q, kc, vc, idx, cu_k, d ** -0.5)
+    # relabel the physical pages: same logical KV -> same output
+    relabel = rng.permutation(pages)
+    kc2 = np.empty_like(kc)
+    vc2 = np.empty_like(vc)
+    kc2[relabel] = kc
+    vc2[relabel] = vc
+    out2 = oatt.decode_attention(q, kc2, vc2, relabel[idx].astype(np.int32), cu_k, d ** -0.5)
+    np.testing.assert_allclose(out, out2, atol=1e-14)
+    # decode row b == offset-causal attention with cached_len = kv_len - 1
+    for b in range(3):
+        pg = idx[cu_k[b]:cu_k[b + 1]]
+        ref = _offset_causal_sdpa(q[b : b + 1], kc[pg], vc[pg], kv_lens[b] - 1, d ** -0.5)
+        np.testing.assert_allclose(out[b : b + 1], ref, atol=1e-12)
+
+
+def test_online_softmax_known_answer_lesson41():
+    """resources/lesson-41-flashattention-online-softmax/run_lesson41.py:20-24:
+    scores [1, 2, 5, -1], values [[1,0],[0,1],[2,2],[-1,3]], blocks 1/2/3."""
+    scores = [1.0, 2.0, 5.0, -1.0]
+    values = [[1, 0], [0, 1], [2, 2], [-1, 3]]
+    e = [math.exp(s - 5.0) for s in scores]
+    z = sum(e)
+    naive = [sum(w * v[j] for w, v in zip(e, values)) / z for j in range(2)]
+    for block in (1, 2, 3, 4):
+        out, m, l = oatt.online_softmax(scores, values, block)
+        np.testing.assert_allclose(out, naive, rtol=1e-14)
+        assert m == 5.0
+        np.testing.assert_allclose(l, z, rtol=1e-14)
+
+
+def test_merge_states_split_anywhere_equals_unsplit():
+    rng = np.random.default_rng(11)
+    hq, hkv, d, n = 8, 2, 16, 23
+    q = rng.standard_normal((hq, d))
+    k = rng.standard_normal((n, hkv, d)) * 2.0
+    v = rng.standard_normal((n, hkv, d))
+    full = oatt.attention_one(q[None], k, v, n - 1, d ** -0.5)[0]
+    o_all, lse_all = oatt.partial_state(q, k, v, d ** -0.5)
+    np.testing.assert_allclose(o_all, full, atol=1e-13)
+    for cuts in ([5], [1, 2, 20], [0, 23], [11, 11, 12]):
+        bounds = [0, *cuts, n]
+        parts = [oatt.partial_state(q, k[a:b], v[a:b], d ** -0.5)
+                 for a, b in zip(bounds[:-1], bounds[1:])]
+        o, lse = oatt.merge_states(parts)
+        np.testing.assert_allclose(o, full, atol=1e-13)
+        np.testing.assert_allclose(lse, lse_all, atol=1e-12)
+    # an empty suffix leaves the prefix result unchanged
+    empty = oatt.partial_state(q, k[:0], v[:0], d ** -0.5)
+    assert np.isneginf(empty[1]).all()
+    o, _ = oatt.merge_states([(o_all, lse_all), empty])
+    np.testing.assert_allclose(o, o_all, atol=0)
+
+
+def test_sdpa_cpu_restatement_matches_oracle():
+    rng = np.random.default_rng(2)
+    hq, hkv, d, pages = 8, 2, 96, 64
+    kc = torch.from_numpy(rng.standard_normal((pages, hkv, d)))
+    vc = torch.from_numpy(rng.standard_normal((pages, hkv, d)))
+    q_lens, kv_lens = [3, 1, 5], [3, 9, 12]
+    idx = torch.from_numpy(rng.permutation(pages)[: sum(kv_lens)].astype(np.int32))
+    cu_q = metadata.cumulative(q_lens)
+    cu_k = metadata.cumulative(kv_lens)
+    q = torch.from_numpy(rng.standard_normal((sum(q_lens), hq, d)))
+    got = paged_attention_cpu(q, kc, vc, idx, cu_q, cu_k, d ** -0.5)
+    ref = oatt.paged_attention(q.numpy(), kc.numpy(), vc.numpy(), idx.numpy(), cu_q, cu_k,
+                               d ** -0.5)
+    np.testing.assert_allclose(got.numpy(), ref.reshape(sum(q_lens), -1), atol=1e-12)
+    with pytest.raises(ValueError, match="cached_len"):
+        sdpa_prefill_attention(q[:2], kc[:3], vc[:3], cached_len=2, sm_scale=1.0)
+
+
+def test_op_test_golden_fixture():
+    """The seeded op-test workload regenerates bit-identically and the oracle
+    reproduces the committed output."""
+    fx = np.load(os.path.join(GOLDEN, "op_test_decode.npz"))
+    wl = make_decode_workload(OP_TEST, seed=int(fx["seed"]))
+    bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(bits(wl.q[0]), fx["q_bits"])
+    assert np.array_equal(bits(wl.k_cache[0]), fx["k_bits"])
+    assert np.array_equal(bits(wl.v_cache[0]), fx["v_bits"])
+    assert np.array_equal(wl.indices.numpy(), fx["indices"])
+    assert np.array_equal(wl.cu_k.numpy(), fx["cu_k"])
+    # every row shares the same 24 prefix pages
+    cu = fx["cu_k"]
+    pre = [fx["indices"][cu[b]: cu[b] + 24].tolist() for b in range(8)]
+    assert all(p == pre[0] for p in pre)
+    f64 = lambda t: t.to(torch.float64).numpy()
+    out = oatt.decode_attention(f64(wl.q[0]), f64(wl.k_cache[0]), f64(wl.v_cache[0]),
+                                wl.indices.numpy(), wl.cu_k.numpy(), 96 ** -0.5)
+    np.testing.assert_allclose(out, fx["out"], rtol=0, atol=1e-15)
+
+
+# --- prefix reuse ---------------------------------------------------------------
+
+@pytest.mark.parametrize("case", [
+    # resources/lesson-14-prefix-kv-reuse/run_lesson14.py:26-37 (old pages 10.., new 100..)
+    ("same", [1, 2, 3], [1, 2, 3], (3, [10, 11, 12], [], [])),
+    ("append", [1, 2, 3], [1, 2, 3, 4, 5], (3, [10, 11, 12], [], [100, 101])),
+    ("retokenized tail", [1, 2, 3, 4], [1, 2, 8, 9], (2, [10, 11], [12, 13], [100, 101])),
+    ("backspace", [1, 2, 3, 4], [1, 2, 3], (0, [], [10, 11, 12, 13], [100, 101, 102])),
+], ids=lambda c: c[0] if isinstance(c, tuple) else None)
+def test_prefix_plan_known_answers_lesson14(case):
+    _, old, new, expect = case
+    got = prefix.plan_prefix(old, list(range(10, 10 + len(old))), new)
+    assert got[:4] == expect
+
+
+def test_token_lcp():
+    assert prefix.token_lcp([], [1]) == 0
+    assert prefix.token_lcp([1, 2, 3], [1, 2]) == 2
+    assert prefix.token_lcp([4], [5]) == 0
+
+
+# --- model oracle building blocks ----------------------------------------------
+
+def test_rope_closed_forms():
+    rng = torch.Generator().manual_seed(0)
+    x = torch.randn(1, 5, 2, 8, generator=rng)
+    pos = torch.tensor([0, 1, 2, 7, 100])
+    y = _rope(x, pos, 10000.0)
+    assert torch.allclose(y[:, 0], x[:, 0])  # position 0 is the identity
+    assert torch.allclose(y.norm(dim=-1), x.norm(dim=-1), atol=1e-5)  # rotation
+    # pair (i, i + D/2) rotates by pos * theta^(-2i/D)
+    for p_i, p in enumerate(pos.tolist()):
+        for i in range(4):
+            ang = p * 10000.0 ** (-2 * i / 8)
+            a, b = x[0, p_i, 0, i].item(), x[0, p_i, 0, i + 4].item()
+            assert abs(y[0, p_i, 0, i].item() - (a * math.cos(ang) - b * math.sin(ang))) < 1e-4
+            assert abs(y[0, p_i, 0, i + 4].item() - (b * math.cos(ang) + a * math.sin(ang))) < 1e-4
+
+
+def _tiny_config(**kw):
+    from aios_amd.config import ModelConfig
+
+    base = dict(num_layers=2, num_qo_heads=4, num_kv_heads=2, head_dim=16, hidden_size=32,
+                vocab_size=50, intermediate_size=24, rms_norm_eps=1e-6)
+    base.update(kw)
+    return ModelConfig(**base)
+
+
+def test_oracle_model_zero_blocks_is_normalised_embedding():
+    """With every projection zero the decoder is the identity on the residual:
+    logits = RMSNorm(embed[ids]) @ embed^T."""
+    from aios_amd.qwen3 import init_weights
+
+    c = _tiny_config()
+    w = init_weights(c, 0, "cpu", dtype=torch.float32, std=0.1)
+    for lw in w["layers"]:
+        for key in ("qkv", "o", "gate_up", "down"):
+            lw[key].zero_()
+    ids = torch.tensor([[3, 7, 7, 1]])
+    e = w["embed"][ids]
+    ref = (e * torch.rsqrt(e.pow(2).mean(-1, keepdim=True) + c.rms_norm_eps)) @ w["embed"].T
+    assert torch.allclose(OracleModel(c, w).logits(ids), ref, atol=1e-5)
+
+
+class _DenseCpuBackend:
+    """Test double for the attention backend: dense offset-causal attention on
+    the CPU via the float64 oracle, no KV cache (one full-sequence prefill)."""
+
+    def __init__(self, scale):
+        self.scale = scale
+
+    def prepare_metadata(self, batch):
+        class _M:
+            def get_last_indices(self, bs):
+                return torch.tensor([batch.input_ids.numel() - 1])
+        batch.attn_metadata = _M()
+
+    def forward(self, q, k, v, kv_cache, layer_id, batch):
+        out = oatt.attention_one(q.double().numpy(), k.double().numpy(), v.double().numpy(), 0,
+                                 self.scale)
+        return torch.from_numpy(out).to(q.dtype).reshape(q.shape[0], -1)
+
+
+def test_oracle_model_matches_product_decoder_composition():
+    """The oracle's plain pre-norm decoder and the product decoder's fused
+    residual-add form (qwen3.py structure) agree in float32 on the CPU."""
+    from aios_amd.core import Batch, Context, Req, SamplingParams, reset_global_ctx, set_global_ctx
+    from aios_amd.qwen3 import Qwen3ForCausalLM, init_weights
+
+    c = _tiny_config(num_layers=3)
+    w = init_weights(c, 1, "cpu", dtype=torch.float32, std=0.2)
+    for lw in w["layers"]:  # non-trivial norm weights
+        for key in ("input_norm", "post_norm", "q_norm", "k_norm"):
+            lw[key].uniform_(0.5, 1.5)
+    ids = torch.tensor([5, 9, 2, 44, 0, 13])
+    backend = _DenseCpuBackend(c.head_dim ** -0.5)
+    model = Qwen3ForCausalLM(c, w, "cpu", attn_backend=backend, max_positions=64)
+    reset_global_ctx()
+    ctx = Context(page_size=1)
+    ctx.kv_cache = None
+    set_global_ctx(ctx)
+    try:
+        req = Req(input_ids=ids, cached_len=0, output_len=1, uid=0,
+                  sampling_params=SamplingParams(), table_idx=0)
+        batch = Batch(reqs=[req], phase="prefill", return_all_logits=True)
+        batch.input_ids = ids
+        batch.positions = torch.arange(len(ids), dtype=torch.int32)
+        backend.prepare_metadata(batch)
+        with ctx.forward_batch(batch):
+            got = model.forward()
+    finally:
+        reset_global_ctx()
+    ref = OracleModel(c, w).logits(ids[None])[0]
+    assert torch.allclose(got, ref, atol=1e-4, rtol=1e-4)
+
+
+def test_top3_by_average_distinct_and_ordered():
+    ids = torch.tensor([[1, 2], [3, 4], [1, 2], [5, 6], [7, 8]])
+    avg = torch.tensor([-1.0, -0.5, -0.2, -3.0, -0.9])
+    assert top3_by_average(ids, avg) == [(1, 2), (3, 4), (7, 8)]
