@@ -29,6 +29,7 @@ EXPORTED_SYMBOLS = (
     "aios_attn_prefill",
     "aios_attn_decode",
     "aios_build_indices",
+    "aios_greedy_select",
 )
 
 
@@ -100,6 +101,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     ]
     lib.aios_build_indices.restype = ctypes.c_int
     lib.aios_build_indices.argtypes = [_vp, _i64, _vp, _vp, _i32, _i32, _vp, _vp]
+    lib.aios_greedy_select.restype = ctypes.c_int
+    lib.aios_greedy_select.argtypes = [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]
 
 
 def lib() -> ctypes.CDLL:

@@ -3,6 +3,7 @@ from .backend import (
     SUPPORTED_HEAD_DIMS,
     Mi355xAttentionBackend,
     Mi355xAttentionMetadata,
+    Mi355xStaticDecodeMetadata,
 )
 
 __all__ = [
@@ -11,5 +12,6 @@ __all__ = [
     "HybridAttentionBackend",
     "Mi355xAttentionBackend",
     "Mi355xAttentionMetadata",
+    "Mi355xStaticDecodeMetadata",
     "SUPPORTED_HEAD_DIMS",
 ]

@@ -61,6 +61,35 @@ class Mi355xAttentionMetadata(BaseAttentionMetadata):
         return self.cu_seqlens_q_gpu[1 : 1 + bs].to(torch.long) - 1
 
 
+@dataclass
+class Mi355xStaticDecodeMetadata(Mi355xAttentionMetadata):
+    """Decode metadata on fixed device buffers, for steps replayed from a HIP graph.
+
+    The plan is built once for ``max_kv_len`` positions per row; the kernels
+    read each row's actual length from ``cu_seqlens_k_gpu``, so one plan (and
+    one captured graph) serves every step whose rows are at most that long.
+    ``refresh(kv_len)`` rewrites cu_seqlens_k and the flat page indices on the
+    device from a device scalar, with no host synchronisation (all rows of the
+    batch have the same length, as in an uncompacted CandidateGroup).
+    """
+
+    row_ids_gpu: torch.Tensor | None = None
+    page_table: torch.Tensor | None = None
+    max_kv_len: int = 0
+    _ramp: torch.Tensor | None = None
+
+    def refresh(self, kv_len: torch.Tensor) -> None:
+        bs = self.row_ids_gpu.numel()
+        torch.mul(self._ramp, kv_len, out=self.cu_seqlens_k_gpu)
+        _lib.check(
+            _lib.lib().aios_build_indices(
+                self.page_table.data_ptr(), self.page_table.stride(0), self.row_ids_gpu.data_ptr(),
+                self.cu_seqlens_k_gpu.data_ptr(), bs, bs * self.max_kv_len,
+                self.indices.data_ptr(), torch.cuda.current_stream(self.indices.device).cuda_stream),
+            "aios_build_indices",
+        )
+
+
 class Mi355xAttentionBackend(BaseAttentionBackend):
     """Paged prefill/decode on hand-written gfx950 HIP kernels."""
 
@@ -200,6 +229,51 @@ class Mi355xAttentionBackend(BaseAttentionBackend):
             self._get_workspace(device)
         batch.attn_metadata = metadata
         return metadata
+
+    def prepare_static_decode(self, row_ids: torch.Tensor, max_kv_len: int, shared_prefix_len: int,
+                              page_table: torch.Tensor) -> Mi355xStaticDecodeMetadata:
+        """Fixed-buffer decode metadata for graph-replayed steps (see
+        :class:`Mi355xStaticDecodeMetadata`); ``shared_prefix_len`` may be any
+        length up to the prefix every row really shares."""
+        bs = row_ids.numel()
+        device = page_table.device
+        if page_table.dtype != torch.int32 or max_kv_len > page_table.shape[1]:
+            raise ValueError("max_kv_len exceeds the page-table row length")
+        cu_q = torch.arange(bs + 1, dtype=torch.int32)
+        cu_k = cu_q * max_kv_len
+        plan = _lib.AttnPlan()
+        _lib.check(
+            _lib.lib().aios_attn_plan(_lib.PHASE_DECODE, cu_q.data_ptr(), cu_k.data_ptr(), bs,
+                                      self.num_heads, self.num_kv_heads, self.head_dim, 1,
+                                      shared_prefix_len, self.workspace_size,
+                                      self.prefix_chunk_len, self.suffix_split_len, plan),
+            "aios_attn_plan",
+        )
+        if plan.ws_bytes:
+            self._get_workspace(device)
+        ramp = torch.arange(bs + 1, dtype=torch.int32, device=device)
+        return Mi355xStaticDecodeMetadata(
+            cu_seqlens_q_cpu=cu_q,
+            cu_seqlens_k_cpu=cu_k,
+            cu_seqlens_q_gpu=ramp.clone(),
+            cu_seqlens_k_gpu=torch.zeros(bs + 1, dtype=torch.int32, device=device),
+            indices=torch.zeros(bs * max_kv_len, dtype=torch.int32, device=device),
+            last_page_len_cpu=self._get_ones_cpu(bs),
+            num_qo_heads=self.num_heads,
+            num_kv_heads=self.num_kv_heads,
+            head_dim=self.head_dim,
+            page_size=1,
+            pos_encoding_mode="NONE",
+            seq_lens_cpu=torch.full((bs,), max_kv_len, dtype=torch.int32),
+            dtype=torch.bfloat16,
+            plan=plan,
+            shared_prefix_len=shared_prefix_len,
+            host_staging=cu_q,
+            row_ids_gpu=row_ids.to(device=device, dtype=torch.int32).contiguous(),
+            page_table=page_table,
+            max_kv_len=max_kv_len,
+            _ramp=ramp,
+        )
 
     def forward(
         self,

@@ -319,4 +319,20 @@ int aios_build_indices(const int32_t* page_table, int64_t page_table_stride,
                    "build_indices launch");
 }
 
+int aios_greedy_select(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                       int32_t elem_bytes, int64_t* token_out, float* logprob_out,
+                       void* stream) {
+  if (rows < 0 || vocab <= 0 || row_stride < vocab)
+    return fail(AIOS_ERR_INVALID, "greedy_select: bad sizes (rows=%d vocab=%d stride=%lld)", rows,
+                vocab, (long long)row_stride);
+  if (elem_bytes != 2 && elem_bytes != 4)
+    return fail(AIOS_ERR_UNSUPPORTED, "greedy_select: elem_bytes %d", elem_bytes);
+  if (rows == 0) return AIOS_OK;
+  if (!logits || !token_out || !logprob_out)
+    return fail(AIOS_ERR_INVALID, "greedy_select: null pointer");
+  return check_hip(aios::greedy_select(logits, row_stride, rows, vocab, elem_bytes, token_out,
+                                       logprob_out, static_cast<hipStream_t>(stream)),
+                   "greedy_select launch");
+}
+
 }  // extern "C"

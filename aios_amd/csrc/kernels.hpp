@@ -75,6 +75,10 @@ hipError_t build_indices(const int32_t* page_table, int64_t pt_stride, const int
                          const int32_t* cu_k, int32_t batch, int32_t max_len,
                          int32_t* indices, hipStream_t stream);
 
+hipError_t greedy_select(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                         int32_t elem_bytes, int64_t* token_out, float* logprob_out,
+                         hipStream_t stream);
+
 // KV positions each 16-lane DPP row of a suffix wavefront holds per pass
 // (4 * tpg positions per pass), sized so the K/V slices fit the registers.
 __host__ __device__ constexpr int suffix_tpg(int D, int G) {

@@ -16,8 +16,10 @@ Restates the GPU control flow of ImeCompletionEngine (python/aios/ime.py):
     decode step (:174-184, :971-973).
 Text governance and sampling are not restated (no tokenizer ships with the
 synthetic models): candidate i starts from the i-th most likely first token
-and then decodes greedily; candidates are ranked by average raw log-prob
-(the reference's base score before text penalties, :1109-1115).
+and then decodes greedily (argmax of the logits, with the raw log-prob of
+the chosen token, sample.py:73, 115-117, on the device kernel
+aios_greedy_select); candidates are ranked by average raw log-prob (the
+reference's base score before text penalties, :1109-1115).
 """
 from __future__ import annotations
 
@@ -30,6 +32,7 @@ import torch
 from aios_amd.config import ModelConfig
 from aios_amd.core import Batch, Context, Req, SamplingParams, reset_global_ctx, set_global_ctx
 from aios_amd.kvcache import MHAKVCache
+from aios_amd.paged import greedy_select
 from aios_amd.qwen3 import Qwen3ForCausalLM
 from aios_amd.scheduler import CacheManager
 
@@ -130,12 +133,25 @@ class CandidateGroupRuntime:
         self.ctx = Context(page_size=1)
         self.ctx.kv_cache = self.kv_cache
         self.ctx.attn_backend = backend
+        # One page-table row per candidate, as long as the rotary table; kept
+        # for the runtime's life so replayed graphs see a fixed address.
+        self.max_context = self.model.rotary.cos.shape[0]
+        self.page_table = torch.zeros((max_attempts, self.max_context), dtype=torch.int32,
+                                      device=self.device)
+        self.ctx.page_table = self.page_table
         set_global_ctx(self.ctx)
 
 
 class CandidateGroupEngine:
-    def __init__(self, rt: CandidateGroupRuntime) -> None:
+    """``use_graphs`` (default) replays each decode step from a HIP graph
+    captured once per (rows, steps, planned prefix, KV capacity); rows that
+    hit EOS are then masked instead of compacted.  ``use_graphs=False`` runs
+    the eager loop with the reference's row compaction."""
+
+    def __init__(self, rt: CandidateGroupRuntime, use_graphs: bool = True) -> None:
         self.rt = rt
+        self.use_graphs = use_graphs
+        self._graphs: dict[tuple, _DecodeGraph] = {}
         self._generation_id = 0
         self._active: CancellationToken | None = None
         self._gen_lock = threading.Lock()
@@ -183,15 +199,14 @@ class CandidateGroupEngine:
                                     (time.perf_counter() - wall) * 1e3, 0.0, 0, True)
         p = len(token_ids)
         max_total = p + config.max_new_tokens
-        if max_total > self.rt.config.max_position_embeddings:
+        if max_total > min(self.rt.config.max_position_embeddings, self.rt.max_context):
             raise ValueError("prefix + output exceeds context limit")
         required = p + n * max(0, config.max_new_tokens - 1)
         if required > self.rt.num_pages:
             raise ValueError(
                 f"CandidateGroup KV budget is too small: need up to {required} pages, "
                 f"configured {self.rt.num_pages}")
-        dev = self.rt.device
-        page_table = torch.zeros((self.rt.max_attempts, max_total), dtype=torch.int32, device=dev)
+        page_table = self.rt.page_table
         self.rt.ctx.page_table = page_table
         started = torch.cuda.Event(enable_timing=True)
         ended = torch.cuda.Event(enable_timing=True)
@@ -199,7 +214,8 @@ class CandidateGroupEngine:
         allocated: list[torch.Tensor] = []
         try:
             prefix_logits, prefix_pages, reused = self._prepare_prefix(token_ids, page_table)
-            raw, allocated, generated, active_tokens, cancelled = self._generate(
+            generate = self._generate_graphed if self.use_graphs else self._generate
+            raw, allocated, generated, active_tokens, cancelled = generate(
                 prefix_logits, page_table, p, config, cancellation)
             unique_pages = len(prefix_pages) + sum(len(a) for a in allocated)
             if allocated:
@@ -307,9 +323,7 @@ class CandidateGroupEngine:
                 cancelled = True
                 break
             if step:
-                lp = torch.log_softmax(logits.float(), dim=-1)
-                token = lp.argmax(dim=-1)
-                raw_lp = lp.gather(1, token[:, None]).squeeze(1)
+                token, raw_lp = greedy_select(logits)
             act = torch.tensor(active, dtype=torch.long, device=dev)
             emitted = torch.ones_like(token, dtype=torch.bool)
             if config.eos_token_id is not None:
@@ -341,3 +355,146 @@ class CandidateGroupEngine:
             stop = "eos" if eos[i] else ("cancelled" if cancelled else "max_new_tokens")
             raw.append(Candidate(ids, avg, stop))
         return raw, allocated, int(sum(cnt)), active_tokens, cancelled
+
+    def _generate_graphed(self, prefix_logits, page_table, prefix_len: int, config, cancellation):
+        """The same candidate rule as :meth:`_generate`, with every decode step
+        after the first replayed from a captured graph and no host
+        synchronisation until the group is done."""
+        n = config.num_candidates
+        t_max = config.max_new_tokens
+        if cancellation.cancelled:
+            return ([Candidate((), float("-inf"), "cancelled") for _ in range(n)], [], 0, 0, True)
+        # Plan the prefix in multiples of 64 and the KV capacity up to the next
+        # multiple of 64, so neighbouring prefix lengths share one graph.
+        plan_prefix = (prefix_len // 64) * 64
+        kv_cap = min(-(-(prefix_len + t_max) // 64) * 64, self.rt.max_context)
+        key = (n, t_max, plan_prefix, kv_cap, config.eos_token_id)
+        g = self._graphs.get(key)
+        if g is None:
+            g = _DecodeGraph(self, n, t_max, plan_prefix, kv_cap, config.eos_token_id)
+            self._graphs[key] = g
+        allocated = []
+        if t_max > 1:
+            pages = self.rt.cache_manager.allocate(n * (t_max - 1))
+            allocated.append(pages)
+            g.pages[: t_max - 1].copy_(pages.view(t_max - 1, n))
+        g.start(prefix_logits, prefix_len)
+        cancelled = False
+        for _ in range(t_max - 1):
+            if cancellation.cancelled:  # observed between steps (ime.py:971-973)
+                cancelled = True
+                break
+            g.run_step()
+        ids = g.out_ids.cpu()
+        cnt = g.counts.cpu().tolist()
+        sums = g.logp_sum.cpu().tolist()
+        eos = g.eos_hit.cpu().tolist()
+        fed = int(g.fed.item())
+        raw = []
+        for i in range(n):
+            row = tuple(int(x) for x in ids[i][ids[i] >= 0].tolist())
+            avg = sums[i] / cnt[i] if cnt[i] else float("-inf")
+            stop = "eos" if eos[i] else ("cancelled" if cancelled else "max_new_tokens")
+            raw.append(Candidate(row, avg, stop))
+        return raw, allocated, int(sum(cnt)), fed, cancelled
+
+
+class _DecodeGraph:
+    """Fixed buffers and the captured decode step of one CandidateGroup shape.
+
+    State on the device: ``tokens`` (the token each row feeds next), ``pos``
+    (its position), ``step`` (index of the fed token), the pre-allocated
+    pages of every step (``pages[s]`` receives the K/V of step s, the order
+    in which the reference allocates one page per row per step), outputs and
+    score sums.  One replay writes the page-table column, refreshes the
+    decode metadata, runs the model, takes the argmax and advances the state.
+    """
+
+    def __init__(self, eng: "CandidateGroupEngine", rows: int, steps: int, plan_prefix: int,
+                 kv_cap: int, eos: int | None) -> None:
+        rt = eng.rt
+        dev = rt.device
+        self.rt = rt
+        self.rows = rows
+        self.steps = steps
+        self.eos = eos
+        self.tokens = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(rows, dtype=torch.int32, device=dev)
+        self.step = torch.zeros(1, dtype=torch.long, device=dev)
+        self.pages = torch.zeros((max(steps - 1, 1), rows), dtype=torch.int32, device=dev)
+        self.out_ids = torch.full((rows, steps), -1, dtype=torch.long, device=dev)
+        self.logp_sum = torch.zeros(rows, dtype=torch.float32, device=dev)
+        self.counts = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.finished = torch.zeros(rows, dtype=torch.bool, device=dev)
+        self.eos_hit = torch.zeros(rows, dtype=torch.bool, device=dev)
+        self.fed = torch.zeros(1, dtype=torch.long, device=dev)
+        self.row_ids = torch.arange(rows, dtype=torch.long, device=dev)
+        self.md = rt.model.attn_backend.prepare_static_decode(self.row_ids, kv_cap, plan_prefix,
+                                                              rt.page_table)
+        reqs = [Req(input_ids=torch.empty(1), cached_len=0, output_len=1, uid=r,
+                    sampling_params=SamplingParams(max_tokens=1), table_idx=r)
+                for r in range(rows)]
+        self.batch = Batch(reqs=reqs, phase="decode")
+        self.batch.input_ids = self.tokens
+        self.batch.positions = self.pos
+        self.batch.attn_metadata = self.md
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    def start(self, prefix_logits: torch.Tensor, prefix_len: int) -> None:
+        """Step 0: candidate i takes the i-th most likely first token."""
+        lp0 = torch.log_softmax(prefix_logits[0].float(), dim=-1)
+        top = torch.topk(lp0, self.rows)
+        tok = top.indices
+        emitted = torch.ones_like(tok, dtype=torch.bool) if self.eos is None else tok.ne(self.eos)
+        self.tokens.copy_(tok)
+        self.out_ids.fill_(-1)
+        self.out_ids[:, 0] = torch.where(emitted, tok, torch.full_like(tok, -1))
+        self.logp_sum.copy_(torch.where(emitted, top.values, torch.zeros_like(top.values)))
+        self.counts.copy_(emitted.long())
+        self.finished.copy_(~emitted)
+        self.eos_hit.copy_(~emitted)
+        self.fed.zero_()
+        self.pos.fill_(prefix_len)
+        self.step.zero_()
+
+    def _body(self) -> None:
+        rt = self.rt
+        out_loc = self.pages.index_select(0, self.step).view(-1)
+        rt.page_table.index_put_((self.row_ids, self.pos.long()), out_loc)
+        self.md.refresh(self.pos[:1] + 1)
+        self.batch.out_loc = out_loc
+        with rt.ctx.forward_batch(self.batch):
+            logits = rt.model.forward()
+        tok, raw = greedy_select(logits)
+        live = ~self.finished
+        self.fed += live.sum()
+        emitted = live if self.eos is None else live & tok.ne(self.eos)
+        self.out_ids.index_copy_(1, self.step + 1,
+                                 torch.where(emitted, tok, torch.full_like(tok, -1))[:, None])
+        self.logp_sum += torch.where(emitted, raw, torch.zeros_like(raw))
+        self.counts += emitted.long()
+        if self.eos is not None:
+            hit = live & tok.eq(self.eos)
+            self.eos_hit |= hit
+            self.finished |= hit
+        self.tokens.copy_(tok)
+        self.pos += 1
+        self.step += 1
+
+    def run_step(self) -> None:
+        if self.graph is not None:
+            self.graph.replay()
+            return
+        # First use: run this step eagerly on the capture stream (which also
+        # warms every library call there), then capture it for the next ones.
+        dev = self.rt.device
+        cur = torch.cuda.current_stream(dev)
+        stream = torch.cuda.Stream(dev)
+        stream.wait_stream(cur)
+        with torch.cuda.stream(stream):
+            self._body()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            self._body()
+        cur.wait_stream(stream)
+        self.graph = graph

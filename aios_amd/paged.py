@@ -140,6 +140,25 @@ def build_indices(page_table: torch.Tensor, row_ids: torch.Tensor, cu_k: torch.T
     return out
 
 
+def greedy_select(logits: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Greedy token per row and its raw log-probability (aios_greedy_select):
+    (argmax(logits, -1) as int64, log_softmax(logits.float())[token] as fp32)."""
+    if logits.ndim != 2 or logits.stride(1) != 1 or not logits.is_cuda:
+        raise ValueError("logits must be a 2-D GPU tensor with contiguous rows")
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("logits must be bfloat16 or float32")
+    rows, vocab = logits.shape
+    tok = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    lp = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    _lib.check(
+        _lib.lib().aios_greedy_select(logits.data_ptr(), logits.stride(0), rows, vocab,
+                                      logits.element_size(), tok.data_ptr(), lp.data_ptr(),
+                                      _stream(logits.device)),
+        "aios_greedy_select",
+    )
+    return tok, lp
+
+
 class BoundCall:
     """A C-ABI launch with its arguments converted once.
 

@@ -24,6 +24,11 @@
  *   aios_build_indices the device half of prepare_metadata's
  *                      torch.cat([page_table[row, :device_len] ...])
  *                      (python/aios/attention/flashinfer.py:228-230)
+ *   aios_greedy_select the greedy branch of Sampler.sample_with_logprobs
+ *                      (python/aios/engine/sample.py:73, 115-117): argmax of
+ *                      the logits plus the raw log_softmax value gathered
+ *                      there, as called by the CandidateGroup decode loop
+ *                      (python/aios/ime.py:998-1008)
  */
 #ifndef AIOS_ATTN_H
 #define AIOS_ATTN_H
@@ -166,6 +171,17 @@ int aios_build_indices(const int32_t* page_table, int64_t page_table_stride,
                        const int32_t* row_ids, const int32_t* cu_k,
                        int32_t batch_size, int32_t total_kv,
                        int32_t* indices_out, void* stream);
+
+/*
+ * Greedy selection over rows of logits (elem_bytes 2: bf16, 4: fp32):
+ *   token_out[r]   = first index of the maximum of logits[r, 0 .. vocab)
+ *   logprob_out[r] = logits[r, token] - logsumexp(logits[r, :])  (fp32)
+ * Rows are row_stride elements apart.  token_out is device int64,
+ * logprob_out device fp32.  Replaces sample.py:73, 115-117 (greedy).
+ */
+int aios_greedy_select(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                       int32_t elem_bytes, int64_t* token_out, float* logprob_out,
+                       void* stream);
 
 #ifdef __cplusplus
 }

@@ -42,10 +42,11 @@ def _prefix(seed: int, n: int, vocab: int) -> list[int]:
     return torch.randint(vocab, (n,), generator=g).tolist()
 
 
-def _engine(config, seed, num_pages=1024):
+def _engine(config, seed, num_pages=1024, use_graphs=False):
+    """Eager engines by default: their decode steps can be observed one by one."""
     w = init_weights(config, seed, "cpu")
     rt = CandidateGroupRuntime(config, weights_to(w, "cuda"), "cuda", num_pages=num_pages)
-    return CandidateGroupEngine(rt), OracleModel(config, w)
+    return CandidateGroupEngine(rt, use_graphs=use_graphs), OracleModel(config, w)
 
 
 def _record_decode_logits(eng):
@@ -242,3 +243,78 @@ def test_eos_compaction():
         gap = tf.max(-1).values - tf.gather(1, seq[0][:, None]).squeeze(1)
         assert gap[1:].max().item() <= 2 * LOGIT_TOL_TIGHT
     assert eng.rt.cache_manager.available_size == eng.rt.num_pages - 32
+
+
+def _check_against_oracle(res, om, prefix, n, steps):
+    """Oracle checks that need only the outputs (graph-replayed steps)."""
+    ids = torch.tensor([c.token_ids for c in res.raw_candidates])
+    assert ids.shape == (n, steps)
+    tf = om.teacher_forced(prefix, ids)
+    chosen = tf.gather(2, ids[:, :, None]).squeeze(2)
+    top_vals = tf[0, 0].sort(descending=True).values[:n]
+    assert (chosen[:, 0] - top_vals).abs().max().item() <= 2 * LOGIT_TOL_TIGHT
+    gap = tf[:, 1:].max(-1).values - chosen[:, 1:]
+    assert gap.max().item() <= 2 * LOGIT_TOL_TIGHT
+    avg_gpu = torch.tensor([c.average_logprob for c in res.raw_candidates])
+    assert (chosen.mean(1) - avg_gpu).abs().max().item() <= AVG_LP_TOL
+
+
+def test_graph_replay_matches_eager_minimind_0p1b():
+    """Graph-replayed decode steps give the eager loop's tokens and scores,
+    on the first capture and on replays in later calls, with eager work and
+    synchronisations between them."""
+    c = MINIMIND_0P1B
+    w = init_weights(c, 20260814, "cpu")
+    rt = CandidateGroupRuntime(c, weights_to(w, "cuda"), "cuda", num_pages=1024)
+    eager = CandidateGroupEngine(rt, use_graphs=False)
+    graphed = CandidateGroupEngine(rt, use_graphs=True)
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=16)
+    om = OracleModel(c, w)
+    for seed in (20260814, 7, 20260814, 8):
+        prefix = _prefix(seed, 32, c.vocab_size)
+        e = eager.complete(prefix, cfg)
+        eager.reset_prefix_cache()
+        torch.cuda.synchronize()
+        g = graphed.complete(prefix, cfg)
+        graphed.reset_prefix_cache()
+        assert [x.token_ids for x in g.raw_candidates] == [x.token_ids for x in e.raw_candidates]
+        assert [x.average_logprob for x in g.raw_candidates] == \
+            [x.average_logprob for x in e.raw_candidates]
+        assert g.active_model_tokens == e.active_model_tokens == 32 + 8 * 15
+        _check_against_oracle(g, om, prefix, 8, 16)
+    assert len(graphed._graphs) == 1
+    assert rt.cache_manager.available_size == rt.num_pages
+
+
+def test_graph_replay_cascade_prefix_and_neighbouring_lengths():
+    """Long prefixes: the graph plans the cascade on a 64-aligned prefix and
+    serves neighbouring prefix lengths from one capture."""
+    c = replace(QWEN3_0P6B, num_layers=3, vocab_size=8192)
+    eng, om = _engine(c, 12, use_graphs=True)
+    for plen in (200, 201, 230):
+        prefix = _prefix(plen, plen, c.vocab_size)
+        res = eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=6))
+        _check_against_oracle(res, om, prefix, 8, 6)
+        eng.reset_prefix_cache()
+    assert len(eng._graphs) == 1
+
+
+def test_graph_replay_eos_masks_rows():
+    c = MINIMIND_0P1B.with_layers(4)
+    eng, om = _engine(c, 9, use_graphs=True)
+    prefix = _prefix(9, 32, c.vocab_size)
+    first = eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=6))
+    eos = first.raw_candidates[2].token_ids[0]
+    res = eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=6,
+                                                    eos_token_id=eos))
+    assert res.raw_candidates[2].token_ids == () and res.raw_candidates[2].stop_reason == "eos"
+    for i, cand in enumerate(res.raw_candidates):
+        assert eos not in cand.token_ids
+        if i == 2 or not cand.token_ids:
+            continue
+        seq = torch.tensor([cand.token_ids])
+        tf = om.teacher_forced(prefix, seq)[0]
+        gap = tf.max(-1).values - tf.gather(1, seq[0][:, None]).squeeze(1)
+        assert gap[1:].max().item() <= 2 * LOGIT_TOL_TIGHT
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages - 32
+
