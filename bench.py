@@ -11,9 +11,14 @@ the timed region; the per-batch plan is built once before it (it is host-only
 work done once per batch by prepare_metadata).
 
 Prints one JSON line: value = decode-step microseconds (lower is better),
-with the main decode kernel's roofline measured live with HIP events, and the
-reference's CPU attention path (restated, oracle/sdpa_cpu.py) timed on a
-bounded sample on the host cores.
+with the main decode kernel's roofline measured live with HIP events, the
+full-model CandidateGroup Top-3 latency of the MiniMind-0.1B-shaped model
+(``candidate_group``: p50/p95 over 30 seeded prefixes after 5 warmups, with
+graph-replayed and eager decode steps), and the reference's CPU attention
+path (restated, oracle/sdpa_cpu.py) timed on a bounded sample on the host
+cores.  ``roofline.traffic`` is the HBM bytes per launch measured with
+rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by a plain-copy
+calibration), read from profiles/traffic.json.
 """
 from __future__ import annotations
 
@@ -29,6 +34,11 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0
+
+
+def _log(msg: str) -> None:
+    """Progress line on stderr (stdout carries only the JSON result)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def _cpu_model() -> str:
@@ -51,6 +61,18 @@ def _traffic(kernel: str):
         return data.get(kernel, {}).get("bytes_per_launch")
     except (ValueError, OSError):
         return None
+
+
+class _HostLayer:
+    """Layer 0 of a workload copied to the host (for the CPU baseline)."""
+
+    def __init__(self, wl) -> None:
+        self.shape = wl.shape
+        self.q = wl.q[:1].cpu()
+        self.k_cache = wl.k_cache[:1].cpu()
+        self.v_cache = wl.v_cache[:1].cpu()
+        self.indices = wl.indices
+        self.cu_k = wl.cu_k
 
 
 def cpu_baseline(wl, max_seconds: float) -> dict:
@@ -97,6 +119,63 @@ def cpu_baseline(wl, max_seconds: float) -> dict:
     }
 
 
+def candidate_group(seed: int, runs: int = 30, warmups: int = 5) -> dict:
+    """Full CandidateGroup Top-3 latency of the MiniMind-0.1B-shaped model.
+
+    14 layers, hidden 768, 8q/2kv heads of 96, SwiGLU 2048, vocab 6400, seeded
+    N(0, 0.02) bf16 weights.  One run = complete(): prefill a 32-token prefix
+    of seeded random ids, then 8 candidates x 16 greedy steps over the shared
+    prefix KV, Top-3 by average log-prob (the reference protocol of
+    bench_ime.py:75-76, 170-196 without text governance).  ``warmups`` runs on
+    other prefixes come first (the first one captures the decode-step graph);
+    each run starts from an empty prefix cache.
+    """
+    import statistics
+
+    import torch
+
+    from aios_amd.config import MINIMIND_0P1B
+    from aios_amd.core import reset_global_ctx
+    from aios_amd.ime import CandidateGroupConfig, CandidateGroupEngine, CandidateGroupRuntime
+    from aios_amd.qwen3 import init_weights
+
+    c = MINIMIND_0P1B
+    rt = CandidateGroupRuntime(c, init_weights(c, seed, "cuda"), "cuda", num_pages=2048)
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=16)
+    out = {"model": "minimind-0.1b-shaped (14L, 768, 8q/2kv x 96, ffn 2048, vocab 6400)",
+           "prefix_tokens": 32, "candidates": 8, "decode_steps": 16, "runs": runs,
+           "warmups": warmups}
+    for mode in ("graph", "eager"):
+        eng = CandidateGroupEngine(rt, use_graphs=mode == "graph")
+        lat, gpu, gen = [], [], 0
+        first = None
+        for i in range(warmups + runs):
+            g = torch.Generator().manual_seed(seed + 1000 + i)
+            prefix = torch.randint(c.vocab_size, (32,), generator=g).tolist()
+            eng.reset_prefix_cache()
+            t0 = time.perf_counter()
+            r = eng.complete(prefix, cfg)
+            dt = (time.perf_counter() - t0) * 1e3
+            if first is None:
+                first = dt
+            if i >= warmups:
+                lat.append(dt)
+                gpu.append(r.gpu_latency_ms)
+                gen += r.generated_tokens
+        eng.reset_prefix_cache()
+        lat.sort()
+        p50 = statistics.median(lat)
+        out[mode] = {"top3_p50_ms": round(p50, 3),
+                     "top3_p95_ms": round(lat[max(0, int(round(0.95 * len(lat))) - 1)], 3),
+                     "gpu_event_p50_ms": round(statistics.median(gpu), 3),
+                     "first_call_ms": round(first, 3),
+                     "candidate_tokens_per_s": round(gen / (sum(lat) * 1e-3), 1)}
+    del rt
+    reset_global_ctx()
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -107,6 +186,10 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--chunk", type=int, default=0, help="prefix chunk override (tuning)")
+    ap.add_argument("--no-candidate-group", action="store_true",
+                    help="skip the full-model CandidateGroup Top-3 latency")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 256 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs the "
@@ -122,6 +205,7 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     shape = SHAPES[args.workload]
+    _log(f"building {shape.name} workload")
     wl = make_decode_workload(shape, seed=args.seed, device=dev, extra_token=True)
     n, nl = shape.num_rows, shape.num_layers
     hq, hkv, d = shape.num_qo_heads, shape.num_kv_heads, shape.head_dim
@@ -210,6 +294,7 @@ def main() -> int:
     torch.cuda.synchronize()
     max_diff = float((ref0.float() - out[0].float()).abs().max())
 
+    cpu_wl = _HostLayer(wl) if not args.no_cpu_baseline else None
     b_kv = 2 * hkv * d * 2
     # Main launch: prefix K/V once, every row's suffix K/V, Q and the page ids.
     sum_s = sum(wl.suffix_lens)
@@ -250,7 +335,7 @@ def main() -> int:
                       "kv_append": round(app_ms * 1e3, 3)},
         "check_max_abs_diff_vs_unshared": max_diff,
         "roofline": {
-            "kernel": "decode_main_kernel<128,4,8> (prefix chunks + suffix items)",
+            "kernel": f"decode_main_kernel<{d}, {hq // hkv}> (prefix chunks + suffix items)",
             "bound": "hbm",
             "achieved": round(casc_gbps, 1),
             "peak": HBM_PEAK_GBPS,
@@ -261,8 +346,22 @@ def main() -> int:
             "avg_launch_us": round(casc_ms * 1e3, 3),
         },
     }
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    del wl, out, ws, ws2, k_new, v_new, app, main_calls, comb_calls, graph
+    torch.cuda.empty_cache()
+    _log(f"decode step {ms_per_step * 1e3:.1f} us; main kernel {casc_ms * 1e3:.2f} us")
+    if not args.no_candidate_group:
+        result["candidate_group"] = candidate_group(args.seed)
+        _log(f"candidate group {result['candidate_group']['graph']['top3_p50_ms']} ms p50")
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(cpu_wl, args.cpu_seconds)
+        _log("cpu baseline done")
     print(json.dumps(result), flush=True)
     return 0
 
