@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "aios_attn_plan",
     "aios_attn_prefill",
     "aios_attn_decode",
+    "aios_attn_append_decode",
     "aios_build_indices",
     "aios_greedy_select",
 )
@@ -59,6 +60,8 @@ class AttnPlan(ctypes.Structure):
         ("prefill_q_tile", ctypes.c_int32),
         ("num_q_tiles", ctypes.c_int32),
         ("stage_mask", ctypes.c_int32),
+        ("min_kv_len", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32),
         ("ws_parts_o", ctypes.c_int64),
         ("ws_parts_lse", ctypes.c_int64),
         ("ws_bytes", ctypes.c_int64),
@@ -98,6 +101,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.aios_attn_decode.restype = ctypes.c_int
     lib.aios_attn_decode.argtypes = [
         ctypes.POINTER(AttnPlan), _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _f32, _vp,
+    ]
+    lib.aios_attn_append_decode.restype = ctypes.c_int
+    lib.aios_attn_append_decode.argtypes = [
+        ctypes.POINTER(AttnPlan), _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp,
+        _vp, _vp, _i64, _f32, _vp,
     ]
     lib.aios_build_indices.restype = ctypes.c_int
     lib.aios_build_indices.argtypes = [_vp, _i64, _vp, _vp, _i32, _i32, _vp, _vp]

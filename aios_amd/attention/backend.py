@@ -10,7 +10,8 @@ Public surface follows python/aios/attention/flashinfer.py:94-394:
   happen once per batch and are reused by every layer).
 * ``forward(q, k, v, kv_cache, layer_id, batch)`` appends the new K/V rows
   (kernel (a)) and then runs prefill (kernel (b)) or decode (kernels (c),
-  (d) and the combine) through the C ABI, returning ``[tokens, Hq*D]``.
+  (d) and the combine) through the C ABI, returning ``[tokens, Hq*D]``; a
+  decode step appends inside the decode launch (aios_attn_append_decode).
 * ``metadata.get_last_indices(bs)`` = ``cu_seqlens_q[1:bs+1] - 1``.
 
 There is one code path for every supported head dim (64, 96, 128), so the
@@ -327,10 +328,26 @@ class Mi355xAttentionBackend(BaseAttentionBackend):
         metadata = batch.attn_metadata
         assert isinstance(metadata, Mi355xAttentionMetadata)
         self._check_q(q)
-        paged_kv_cache.store_kv(k, v, batch.out_loc.view(-1), layer_id)
+        plan = metadata.plan
+        out_loc = batch.out_loc.view(-1)
+        ws = self._get_workspace(q.device) if plan.ws_bytes else None
+        if plan.prefix_len < plan.min_kv_len and out_loc.dtype == torch.int32:
+            # The store_kv of flashinfer.py:389 runs inside the decode launch:
+            # each row's new token is its last KV position.
+            if k.shape != v.shape or k.shape[1:] != (self.num_kv_heads, self.head_dim):
+                raise ValueError("K/V input shape does not match the cache layout")
+            if out_loc.numel() != k.shape[0]:
+                raise ValueError("KV write indices and K/V tensors must have matching token counts")
+            k_cache, v_cache = self._layer_caches(paged_kv_cache, layer_id)
+            out = paged.append_decode(plan, q, k, v, out_loc.contiguous(),
+                                      k_cache.view(-1, self.num_kv_heads, self.head_dim),
+                                      v_cache.view(-1, self.num_kv_heads, self.head_dim),
+                                      metadata.indices, metadata.cu_seqlens_k_gpu, workspace=ws,
+                                      sm_scale=self.sm_scale)
+            return out.reshape(bsz, -1)
+        paged_kv_cache.store_kv(k, v, out_loc, layer_id)
         k_cache, v_cache = self._layer_caches(paged_kv_cache, layer_id)
-        ws = self._get_workspace(q.device) if metadata.plan.ws_bytes else None
-        out = paged.decode(metadata.plan, q, k_cache.view(-1, self.num_kv_heads, self.head_dim),
+        out = paged.decode(plan, q, k_cache.view(-1, self.num_kv_heads, self.head_dim),
                            v_cache.view(-1, self.num_kv_heads, self.head_dim), metadata.indices,
                            metadata.cu_seqlens_k_gpu, workspace=ws, sm_scale=self.sm_scale)
         return out.reshape(bsz, -1)

@@ -1,5 +1,6 @@
 // C ABI of the attention backend: validation, host-side planning and launch.
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -117,6 +118,7 @@ int aios_attn_plan(int32_t phase, const int32_t* cu_q, const int32_t* cu_k, int3
   p->total_kv = cu_k[batch];
   p->max_q_len = max_q;
   p->max_kv_len = max_kv;
+  p->min_kv_len = min_kv;
   const int cus = device_cus();
 
   if (phase == AIOS_PHASE_PREFILL) {
@@ -245,10 +247,22 @@ int aios_attn_prefill(const aios_attn_plan_t* p, const void* q, int64_t q_tok_st
                    "prefill launch");
 }
 
-int aios_attn_decode(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
-                     const void* k_cache, const void* v_cache, int64_t kv_num_pages,
-                     const int32_t* indices, const int32_t* cu_k, void* out, void* workspace,
-                     int64_t workspace_bytes, float sm_scale, void* stream) {
+}  // extern "C"
+
+namespace {
+
+struct NewKV {
+  const void* k;
+  int64_t k_stride;
+  const void* v;
+  int64_t v_stride;
+  const int32_t* out_loc;
+};
+
+int decode_impl(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
+                const void* k_cache, const void* v_cache, int64_t kv_num_pages,
+                const int32_t* indices, const int32_t* cu_k, void* out, void* workspace,
+                int64_t workspace_bytes, float sm_scale, void* stream, const NewKV* nk) {
   int rc = check_plan(p, AIOS_PHASE_DECODE);
   if (rc) return rc;
   if (p->batch_size == 0) return AIOS_OK;
@@ -297,6 +311,30 @@ int aios_attn_decode(const aios_attn_plan_t* p, const void* q, int64_t q_tok_str
   a.parts.n_parts = p->num_parts;
   a.parts.n_chunks = p->num_prefix_chunks;
   a.out = static_cast<aios::bf16*>(out);
+  if (nk) {
+    if (!nk->k || !nk->v || !nk->out_loc)
+      return fail(AIOS_ERR_INVALID, "append_decode: null pointer");
+    if (nk->k_stride < a.kv_tok_stride || nk->v_stride < a.kv_tok_stride ||
+        (nk->k_stride % 8) != 0 || (nk->v_stride % 8) != 0)
+      return fail(AIOS_ERR_INVALID,
+                  "append_decode: K/V token strides must be >= Hkv*D and multiples of 8");
+    const int E = D / 16;
+    const uintptr_t align = E == 8 ? 16 : (E == 4 ? 8 : 4);
+    if (((uintptr_t)nk->k % align) != 0 || ((uintptr_t)nk->v % align) != 0)
+      return fail(AIOS_ERR_INVALID, "append_decode: K/V rows must be %d-byte aligned", (int)align);
+    if (p->min_kv_len < 1 || p->prefix_len >= p->min_kv_len)
+      return fail(AIOS_ERR_INVALID,
+                  "append_decode: every row's new token must lie after the shared prefix");
+    a.k_new = static_cast<const aios::bf16*>(nk->k);
+    a.v_new = static_cast<const aios::bf16*>(nk->v);
+    a.k_new_stride = nk->k_stride;
+    a.v_new_stride = nk->v_stride;
+    a.out_loc = nk->out_loc;
+  }
+  {
+    const char* v = getenv("AIOS_EXP");
+    a.variant = v ? atoi(v) : 0;
+  }
   if (mask & 1) {
     rc = check_hip(aios::launch_decode_main(D, a, s), "decode launch");
     if (rc) return rc;
@@ -304,6 +342,29 @@ int aios_attn_decode(const aios_attn_plan_t* p, const void* q, int64_t q_tok_str
   if (p->num_parts > 1 && (mask & 2))
     return check_hip(aios::launch_decode_combine(D, a, s), "combine launch");
   return AIOS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aios_attn_decode(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
+                     const void* k_cache, const void* v_cache, int64_t kv_num_pages,
+                     const int32_t* indices, const int32_t* cu_k, void* out, void* workspace,
+                     int64_t workspace_bytes, float sm_scale, void* stream) {
+  return decode_impl(p, q, q_tok_stride, k_cache, v_cache, kv_num_pages, indices, cu_k, out,
+                     workspace, workspace_bytes, sm_scale, stream, nullptr);
+}
+
+int aios_attn_append_decode(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
+                            const void* k_new, int64_t k_tok_stride, const void* v_new,
+                            int64_t v_tok_stride, const int32_t* out_loc, void* k_cache,
+                            void* v_cache, int64_t kv_num_pages, const int32_t* indices,
+                            const int32_t* cu_k, void* out, void* workspace,
+                            int64_t workspace_bytes, float sm_scale, void* stream) {
+  const NewKV nk = {k_new, k_tok_stride, v_new, v_tok_stride, out_loc};
+  return decode_impl(p, q, q_tok_stride, k_cache, v_cache, kv_num_pages, indices, cu_k, out,
+                     workspace, workspace_bytes, sm_scale, stream, &nk);
 }
 
 int aios_build_indices(const int32_t* page_table, int64_t page_table_stride,

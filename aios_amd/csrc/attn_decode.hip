@@ -50,6 +50,19 @@ __device__ __forceinline__ Slice<E> load_slice(const bf16* p) {
   return r;
 }
 
+template <int E>
+__device__ __forceinline__ void store_slice(bf16* p, const Slice<E>& s) {
+  if constexpr (E == 8) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(s.w[0], s.w[1], s.w[2], s.w[3]);
+  } else if constexpr (E == 4) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(s.w[0], s.w[1]);
+  } else {
+    uint32_t* q = reinterpret_cast<uint32_t*>(p);
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) q[i] = s.w[i];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // prefix part
 template <int D>
@@ -61,8 +74,12 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
   const int G = a.group;
   const int mg = wg % a.m_groups;
   const int unit = wg / a.m_groups;
-  const int chunk = unit % a.n_chunks;
-  const int h = unit / a.n_chunks;
+  // Consecutive workgroups take different kv-heads: the hardware deals
+  // workgroups round-robin to the XCDs, so with 8 kv-heads every chunk of
+  // one head (and the combine of that head, which uses the same order) runs
+  // on one XCD and its partials stay in that XCD's L2.
+  const int h = unit % a.num_kv_heads;
+  const int chunk = unit / a.num_kv_heads;
 
   TileEngine<D, false> eng;
   eng.min_limit = 0x7fffffff;
@@ -78,13 +95,15 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
     const int g = m - b * G;
     qr[rt] = a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + g) * D;
   }
-  eng.load_q(qr[0], ok[0], qr[1], ok[1]);
   const int kv_begin = chunk * a.chunk_len;
   const int kv_end = min(a.prefix_len, kv_begin + a.chunk_len);
   const int64_t tok_bytes = a.kv_tok_stride * 2;
+  // A wavefront whose 32 rows are all padding only helps stream K/V.
+  const bool active = mg * 128 + wave * 32 < a.m_rows;
   eng.run(lds, reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2,
           reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2, tok_bytes,
-          a.num_pages, a.indices, kv_begin, kv_end, a.scale_log2);
+          a.num_pages, a.indices, kv_begin, kv_end, a.scale_log2,
+          [&] { eng.load_q(qr[0], ok[0], qr[1], ok[1]); }, active);
 
   constexpr int DT = D / 16;
 #pragma unroll
@@ -151,6 +170,10 @@ __device__ __forceinline__ void decode_suffix_item(const DecodeArgs& a, int item
 
   const bf16* kb = a.k_cache + (int64_t)h * D + l16 * E;
   const bf16* vb = a.v_cache + (int64_t)h * D + l16 * E;
+  // Fused append: the row's last position is its new token, taken from
+  // k_new / v_new and written to its page here (no other workgroup of the
+  // launch reads that page).
+  const int t_new = a.k_new != nullptr ? kv_len - 1 : -1;
   for (int t0 = s_begin; t0 < s_end; t0 += 4 * TPG) {
     int64_t page[TPG];
 #pragma unroll
@@ -161,12 +184,39 @@ __device__ __forceinline__ void decode_suffix_item(const DecodeArgs& a, int item
     Slice<E> ks[TPG], vs[TPG];
 #pragma unroll
     for (int u = 0; u < TPG; ++u) {
-      if ((uint64_t)page[u] < (uint64_t)a.num_pages) {
+      if (t0 + 4 * u + lg == t_new) {
+        ks[u] = load_slice<E>(a.k_new + (int64_t)b * a.k_new_stride + (int64_t)h * D + l16 * E);
+        vs[u] = load_slice<E>(a.v_new + (int64_t)b * a.v_new_stride + (int64_t)h * D + l16 * E);
+      } else if ((uint64_t)page[u] < (uint64_t)a.num_pages) {
         ks[u] = load_slice<E>(kb + page[u] * a.kv_tok_stride);
         vs[u] = load_slice<E>(vb + page[u] * a.kv_tok_stride);
       } else {
 #pragma unroll
         for (int i = 0; i < E / 2; ++i) ks[u].w[i] = vs[u].w[i] = 0u;
+      }
+    }
+    if (t_new >= t0 && t_new < t0 + 4 * TPG && (t_new - t0) % 4 == lg) {
+      const int u = (t_new - t0) / 4;
+      const int64_t dst = a.out_loc[b];
+      if ((uint64_t)dst < (uint64_t)a.num_pages) {
+        const int64_t off = dst * a.kv_tok_stride + (int64_t)h * D + l16 * E;
+#pragma unroll
+        for (int uu = 0; uu < TPG; ++uu) {
+          if (uu == u) {
+            store_slice<E>(const_cast<bf16*>(a.k_cache) + off, ks[uu]);
+            store_slice<E>(const_cast<bf16*>(a.v_cache) + off, vs[uu]);
+          }
+        }
+      } else {
+        // The separate append would skip this row and the decode would read
+        // page out_loc[b] as zeros.
+#pragma unroll
+        for (int uu = 0; uu < TPG; ++uu) {
+          if (uu == u) {
+#pragma unroll
+            for (int i = 0; i < E / 2; ++i) ks[uu].w[i] = vs[uu].w[i] = 0u;
+          }
+        }
       }
     }
     float sc[TPG][G];

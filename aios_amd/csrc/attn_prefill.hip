@@ -46,10 +46,14 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
     eng.limit[rt] = cached + i;
   }
   eng.min_limit = cached + qt * a.q_tile;
-  eng.load_q(qr[0], ok[0], qr[1], ok[1]);
+  // A wavefront whose 32 rows are all past the tile's tokens only helps
+  // stream K/V; it skips the math.
+  const int m0 = (threadIdx.x >> 6) * 32;
+  const bool active = m0 < a.q_tile * G && qt * a.q_tile + m0 / G < q_len;
   eng.run(lds, reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2,
           reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2, a.kv_tok_stride * 2,
-          a.num_pages, a.indices + kv_base, 0, min(kv_len, cached + q_hi), a.scale_log2);
+          a.num_pages, a.indices + kv_base, 0, min(kv_len, cached + q_hi), a.scale_log2,
+          [&] { eng.load_q(qr[0], ok[0], qr[1], ok[1]); }, active);
 
   constexpr int DT = D / 16;
 #pragma unroll

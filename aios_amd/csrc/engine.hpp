@@ -107,11 +107,13 @@ struct TileEngine {
 
   // Stream KV positions [kv_begin, kv_end) of one kv-head (kc / vc point at
   // head h of page 0; tok_bytes = page stride) whose page ids are
-  // idx[kv_begin .. kv_end).  Leaves o (unnormalised), m_run and the row
-  // total l_run.
+  // idx[kv_begin .. kv_end).  `qload` loads the Q fragment; an inactive
+  // wavefront (all of its rows padding) streams K/V but skips the math.
+  // Leaves o (unnormalised), m_run and the row total l_run.
+  template <typename QLoad>
   __device__ void run(uint8_t* lds, const uint8_t* kc, const uint8_t* vc, int64_t tok_bytes,
                       int64_t num_pages, const int32_t* idx, int kv_begin, int kv_end,
-                      float scale_log2) {
+                      float scale_log2, QLoad&& qload, bool active = true) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -137,6 +139,10 @@ struct TileEngine {
     };
     stage_ids();
     lds_barrier();
+    // Q is needed only at the first compute: its loads go out after the page
+    // ids (which gate every DMA) and ahead of the DMAs, so the first wait
+    // below covers them.
+    qload();
 
     // Loop-invariant part of every DMA load of this thread: which token of
     // the sub-tile it serves, and the byte offset (rotated chunk) inside that
@@ -196,8 +202,9 @@ struct TileEngine {
         }
         issue(s_next);
       }
-      compute(lds + (it & (kRing - 1)) * T::SUB_BYTES, kv_begin + it * kSubTok, kv_end,
-              scale_log2, l16, lg);
+      if (active)
+        compute(lds + (it & (kRing - 1)) * T::SUB_BYTES, kv_begin + it * kSubTok, kv_end,
+                scale_log2, l16, lg);
     }
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) l_run[rt] = xrow_sum(l_run[rt]);

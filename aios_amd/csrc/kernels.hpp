@@ -46,6 +46,14 @@ struct DecodeArgs {
   int32_t final_out;     // 1: a single part per (row, head): write bf16 out directly
   PartsArgs parts;
   bf16* out;  // [B][Hq][D]
+  // Fused KV append (null k_new: none).  Row b's last KV position is its new
+  // token: read from k_new / v_new and written to page out_loc[b].
+  const bf16* k_new;
+  const bf16* v_new;
+  int64_t k_new_stride;  // elements per token
+  int64_t v_new_stride;
+  const int32_t* out_loc;
+  int32_t variant;
 };
 
 struct PrefillArgs {

@@ -95,6 +95,53 @@ def decode(p: _lib.AttnPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
     return out
 
 
+def _check_new_kv(k: torch.Tensor, v: torch.Tensor, out_loc: torch.Tensor, p: _lib.AttnPlan) -> None:
+    if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16 or not k.is_cuda or not v.is_cuda:
+        raise ValueError("new K/V rows must be bfloat16 GPU tensors")
+    shape = (p.batch_size, p.num_kv_heads, p.head_dim)
+    if tuple(k.shape) != shape or tuple(v.shape) != shape:
+        raise ValueError("K/V input shape does not match the cache layout")
+    for t in (k, v):
+        if t.stride(2) != 1 or t.stride(1) != p.head_dim:
+            raise ValueError("new K/V rows must have contiguous (heads, head_dim) rows")
+    _check_i32(out_loc, "out_loc", p.batch_size)
+
+
+def append_decode(p: _lib.AttnPlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                  out_loc: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  indices: torch.Tensor, cu_k: torch.Tensor, *, out: torch.Tensor | None = None,
+                  workspace: torch.Tensor | None = None,
+                  sm_scale: float | None = None) -> torch.Tensor:
+    """Append each row's new K/V (k[b], v[b] -> page out_loc[b]) and decode, in
+    one launch (aios_attn_append_decode); row b's last KV position must be
+    out_loc[b].  Returns [B, Hq, D] bf16."""
+    if p.phase != _lib.PHASE_DECODE:
+        raise ValueError("plan was not built for decode")
+    _check_q(q, p)
+    if q.shape[0] != p.batch_size:
+        raise ValueError("decode batch must contain one flat token per request")
+    _check_cache(k_cache, p)
+    _check_cache(v_cache, p)
+    _check_i32(indices, "indices", p.total_kv)
+    _check_i32(cu_k, "cu_k", p.batch_size + 1)
+    _check_new_kv(k, v, out_loc, p)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if p.ws_bytes and (workspace is None or workspace.numel() < p.ws_bytes):
+        raise RuntimeError(f"decode needs a workspace of {p.ws_bytes} bytes")
+    scale = p.head_dim ** -0.5 if sm_scale is None else sm_scale
+    _lib.check(
+        _lib.lib().aios_attn_append_decode(
+            p, q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
+            out_loc.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
+            indices.data_ptr(), cu_k.data_ptr(), out.data_ptr(),
+            workspace.data_ptr() if workspace is not None else None,
+            workspace.numel() if workspace is not None else 0, scale, _stream(q.device)),
+        "aios_attn_append_decode",
+    )
+    return out
+
+
 def prefill(p: _lib.AttnPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
             indices: torch.Tensor, cu_q: torch.Tensor, cu_k: torch.Tensor, *,
             out: torch.Tensor | None = None, sm_scale: float | None = None) -> torch.Tensor:
@@ -200,6 +247,35 @@ def bind_decode(p: _lib.AttnPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cach
             workspace.numel() if workspace is not None else 0, ctypes.c_float(scale), s)
     return BoundCall(_lib.lib().aios_attn_decode, args,
                      (p, q, k_cache, v_cache, indices, cu_k, out, workspace))
+
+
+def bind_append_decode(p: _lib.AttnPlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       out_loc: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       indices: torch.Tensor, cu_k: torch.Tensor, out: torch.Tensor,
+                       workspace: torch.Tensor | None, sm_scale: float | None = None,
+                       stream: torch.cuda.Stream | None = None) -> BoundCall:
+    """Checked once, then launched many times: aios_attn_append_decode."""
+    import ctypes
+
+    _check_q(q, p)
+    _check_cache(k_cache, p)
+    _check_cache(v_cache, p)
+    _check_i32(indices, "indices", p.total_kv)
+    _check_i32(cu_k, "cu_k", p.batch_size + 1)
+    _check_new_kv(k, v, out_loc, p)
+    if out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like q")
+    if p.ws_bytes and (workspace is None or workspace.numel() < p.ws_bytes):
+        raise RuntimeError(f"decode needs a workspace of {p.ws_bytes} bytes")
+    scale = p.head_dim ** -0.5 if sm_scale is None else sm_scale
+    s = stream.cuda_stream if stream is not None else _stream(q.device)
+    args = (ctypes.byref(p), q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(),
+            v.stride(0), out_loc.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+            k_cache.shape[0], indices.data_ptr(), cu_k.data_ptr(), out.data_ptr(),
+            workspace.data_ptr() if workspace is not None else None,
+            workspace.numel() if workspace is not None else 0, ctypes.c_float(scale), s)
+    return BoundCall(_lib.lib().aios_attn_append_decode, args,
+                     (p, q, k, v, out_loc, k_cache, v_cache, indices, cu_k, out, workspace))
 
 
 def bind_kv_append(k_cache: torch.Tensor, v_cache: torch.Tensor, out_loc: torch.Tensor,

@@ -21,6 +21,8 @@
  *                      flashinfer.py:300-372, 33-91)
  *   aios_attn_decode   BatchDecodeWithPagedKVCacheWrapper.run (python/aios/
  *                      attention/flashinfer.py:374-394)
+ *   aios_attn_append_decode  store_kv (flashinfer.py:389 -> store.py:32-61)
+ *                      and the decode run above, in one launch
  *   aios_build_indices the device half of prepare_metadata's
  *                      torch.cat([page_table[row, :device_len] ...])
  *                      (python/aios/attention/flashinfer.py:228-230)
@@ -104,6 +106,8 @@ typedef struct aios_attn_plan {
    * suffix items), bit 1 the combine; 0 (the value aios_attn_plan writes)
    * issues both.  Lets a profiler bracket the two launches separately. */
   int32_t stage_mask;
+  int32_t min_kv_len;        /* shortest row of the batch */
+  int32_t reserved0;
   /* workspace layout (byte offsets) */
   int64_t ws_parts_o;
   int64_t ws_parts_lse;
@@ -161,6 +165,30 @@ int aios_attn_decode(const aios_attn_plan_t* plan, const void* q,
                      const int32_t* indices,
                      const int32_t* cu_k, void* out, void* workspace,
                      int64_t workspace_bytes, float sm_scale, void* stream);
+
+/*
+ * Paged KV append and decode in one launch: the same result as
+ *   aios_kv_append(k_cache, v_cache, kv_num_pages, Hkv*D, out_loc, k_new,
+ *                  k_tok_stride, v_new, v_tok_stride, batch_size, Hkv*D, 2)
+ * followed by aios_attn_decode(...), for the decode step of
+ * BatchDecodeWithPagedKVCacheWrapper after MHAKVCache.store_kv
+ * (python/aios/attention/flashinfer.py:374-394 with :389, and
+ * python/aios/kernel/store.py:32-61).  Row b's new token is its last KV
+ * position: indices[cu_k[b+1] - 1] == out_loc[b]; its K/V rows k_new[b],
+ * v_new[b] ([Hkv, D], token strides in elements) are attended to directly
+ * and written to page out_loc[b] (an out_loc outside [0, kv_num_pages) is
+ * not written, and that row then attends to zeros there, as the separate
+ * calls would).  Needs plan->prefix_len < plan->min_kv_len (the new token
+ * is never part of the shared prefix).
+ */
+int aios_attn_append_decode(const aios_attn_plan_t* plan, const void* q,
+                            int64_t q_tok_stride, const void* k_new,
+                            int64_t k_tok_stride, const void* v_new,
+                            int64_t v_tok_stride, const int32_t* out_loc,
+                            void* k_cache, void* v_cache, int64_t kv_num_pages,
+                            const int32_t* indices, const int32_t* cu_k,
+                            void* out, void* workspace, int64_t workspace_bytes,
+                            float sm_scale, void* stream);
 
 /*
  * Gather the flat page-index list of a batch on the device:

@@ -176,9 +176,12 @@ def test_page_permutation_invariance():
     assert torch.equal(out.cpu(), out2.cpu())
 
 
-def test_long_rows_without_shared_prefix():
+@pytest.mark.parametrize("hq,hkv,d,rows,lo,hi", [(16, 8, 128, 3, 1500, 3000),
+                                                 (32, 8, 128, 4, 4000, 4160),
+                                                 (8, 2, 96, 3, 2000, 2500)])
+def test_long_rows_without_shared_prefix(hq, hkv, d, rows, lo, hi):
     # Generic paged decode (no shared prefix): long rows are split and merged.
-    shape = DecodeShape("long_rows", 1, 3, 0, 3000, 16, 8, 128, 16384, min_suffix=1500)
+    shape = DecodeShape("long_rows", 1, rows, 0, hi, hq, hkv, d, 32768, min_suffix=lo)
     wl = make_decode_workload(shape, seed=31)
     out, p = _run(wl, shared=0)
     assert p.num_suffix_splits > 1 and p.num_parts > 1
@@ -194,3 +197,92 @@ def test_single_launch_row_lengths(max_suffix):
     out, p = _run(wl, shared=0)
     assert (p.num_parts == 1) == (max_suffix <= 2 * 4 * p.suffix_tpg)
     np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
+
+
+def _append_decode_case(shape, seed, shared=None, chunk=0, split=0, oob_row=None):
+    wl = make_decode_workload(shape, seed=seed, extra_token=True)
+    n, hkv, d = shape.num_rows, shape.num_kv_heads, shape.head_dim
+    g = torch.Generator().manual_seed(seed + 99)
+    k_new = (torch.randn(n, hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+    # v as a strided view, the way it leaves the fused qkv projection
+    v_big = (torch.randn(n, 3 * hkv, d, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+    v_new = v_big[:, hkv:2 * hkv]
+    last = torch.tensor([int(wl.indices[int(wl.cu_k[i + 1]) - 1]) for i in range(n)],
+                        dtype=torch.int32)
+    if oob_row is not None:
+        last[oob_row] = shape.num_pages + 5
+        wl.indices[int(wl.cu_k[oob_row + 1]) - 1] = shape.num_pages + 5
+    out_loc = last.to(DEV)
+    cu_q = torch.arange(n + 1, dtype=torch.int32)
+    p = paged.plan("decode", cu_q, wl.cu_k, shape.num_qo_heads, hkv, d,
+                   shared_prefix_len=shape.prefix_len if shared is None else shared,
+                   workspace_bytes=64 << 20, prefix_chunk_len=chunk, suffix_split_len=split)
+    ws = torch.empty(max(p.ws_bytes, 256), dtype=torch.uint8, device=DEV)
+    q = wl.q[0].to(DEV)
+    idx = wl.indices.to(DEV)
+    cuk = wl.cu_k.to(DEV)
+    # separate calls: store_cache then decode
+    ka, va = wl.k_cache[0].to(DEV), wl.v_cache[0].to(DEV)
+    from aios_amd.kernel import store_cache
+    store_cache(ka, va, out_loc, k_new, v_new)
+    out_a = paged.decode(p, q, ka, va, idx, cuk, workspace=ws)
+    # one launch
+    kb, vb = wl.k_cache[0].to(DEV), wl.v_cache[0].to(DEV)
+    out_b = paged.append_decode(p, q, k_new, v_new, out_loc, kb, vb, idx, cuk, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(bits_t(ka), bits_t(kb)) and torch.equal(bits_t(va), bits_t(vb))
+    assert torch.equal(out_a, out_b)
+    if oob_row is None:  # (the oracle has no out-of-range page semantics)
+        ref = oatt.decode_attention(to_np64(q), to_np64(ka), to_np64(va), wl.indices.numpy(),
+                                    wl.cu_k.numpy(), d ** -0.5)
+        np.testing.assert_allclose(to_np64(out_b), ref, **BF16_TOL)
+    return p
+
+
+def bits_t(t):
+    return t.contiguous().view(torch.int16)
+
+
+@pytest.mark.parametrize("case", ["op_test", "cascade", "splits", "long_context_layer",
+                                  "h64_g3", "h128_g2", "no_shared"])
+def test_append_decode_matches_separate_calls(case):
+    """KV append inside the decode launch: caches bit-identical and outputs
+    bitwise equal to store_cache followed by decode."""
+    if case == "op_test":
+        p = _append_decode_case(OP_TEST, 20260814)
+        assert p.num_parts == 1
+    elif case == "cascade":
+        p = _append_decode_case(OP_TEST, 3, chunk=32)
+        assert p.prefix_len == 24
+    elif case == "splits":
+        p = _append_decode_case(DecodeShape("sp", 1, 8, 200, 40, 8, 2, 96, 1024), 11, chunk=64,
+                                split=8)
+        assert p.num_suffix_splits > 1
+    elif case == "long_context_layer":
+        shape = DecodeShape("lc1", 1, 24, 4096, 64, 32, 8, 128, 65536)
+        p = _append_decode_case(shape, 20260814)
+        assert p.num_prefix_chunks > 1
+    elif case == "h64_g3":
+        _append_decode_case(DecodeShape("h64", 1, 8, 150, 20, 12, 4, 64, 512), 5)
+    elif case == "h128_g2":
+        _append_decode_case(DecodeShape("h128", 1, 8, 140, 24, 16, 8, 128, 512), 6)
+    else:
+        _append_decode_case(OP_TEST, 9, shared=0)
+
+
+def test_append_decode_out_of_range_slot_matches_separate_calls():
+    _append_decode_case(OP_TEST, 4, chunk=32, oob_row=3)
+
+
+def test_append_decode_rejects_new_token_inside_shared_prefix():
+    shape = DecodeShape("empty_suffix", 1, 8, 40, 0, 8, 2, 96, 256)
+    wl = make_decode_workload(shape, seed=5)
+    n = shape.num_rows
+    p = paged.plan("decode", torch.arange(n + 1, dtype=torch.int32), wl.cu_k, 8, 2, 96,
+                   shared_prefix_len=40, prefix_chunk_len=32)
+    kv = torch.zeros(n, 2, 96, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="after the shared prefix"):
+        paged.append_decode(p, wl.q[0].to(DEV), kv, kv, torch.zeros(n, dtype=torch.int32, device=DEV),
+                            wl.k_cache[0].to(DEV), wl.v_cache[0].to(DEV), wl.indices.to(DEV),
+                            wl.cu_k.to(DEV), workspace=torch.empty(1 << 20, dtype=torch.uint8,
+                                                                   device=DEV))

@@ -34,8 +34,12 @@ def test_library_exports_every_symbol():
 
 
 def test_plan_struct_layout_matches_header():
-    # 22 int32 fields followed by 3 int64 fields.
-    assert ctypes.sizeof(_lib.AttnPlan) == 22 * 4 + 3 * 8
+    text = HEADER.read_text()
+    body = text[text.index("typedef struct aios_attn_plan {"):text.index("} aios_attn_plan_t;")]
+    fields = re.findall(r"^\s*(int32_t|int64_t)\s+(\w+);", body, re.M)
+    ctype = {"int32_t": ctypes.c_int32, "int64_t": ctypes.c_int64}
+    assert [(n, ctype[t]) for t, n in fields] == list(_lib.AttnPlan._fields_)
+    assert ctypes.sizeof(_lib.AttnPlan) == 24 * 4 + 3 * 8
 
 
 def _plan(phase, cu_q, cu_k, hq=8, hkv=2, d=96, shared=0, ws=1 << 26, chunk=0, split=0):
