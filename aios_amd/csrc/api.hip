@@ -310,6 +310,7 @@ int decode_impl(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
   a.parts.lse = reinterpret_cast<float*>(ws + p->ws_parts_lse);
   a.parts.n_parts = p->num_parts;
   a.parts.n_chunks = p->num_prefix_chunks;
+  a.parts.rows = p->batch_size * p->group;
   a.out = static_cast<aios::bf16*>(out);
   if (nk) {
     if (!nk->k || !nk->v || !nk->out_loc)

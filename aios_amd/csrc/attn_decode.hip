@@ -83,6 +83,7 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
 
   TileEngine<D, false> eng;
   eng.min_limit = 0x7fffffff;
+  eng.abl = a.variant >> 4;
   int rows[2];
   bool ok[2];
   const bf16* qr[2];
@@ -106,6 +107,7 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
           [&] { eng.load_q(qr[0], ok[0], qr[1], ok[1]); }, active);
 
   constexpr int DT = D / 16;
+  if (a.variant & 128) return;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const float l_tot = eng.l_run[rt];
@@ -113,19 +115,20 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
     const int m = rows[rt];
     const int b = m / G;
     const int g = m - b * G;
-    const int64_t slot = ((int64_t)b * a.num_kv_heads + h) * a.parts.n_parts + chunk;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    bf16* po = a.parts.o + (slot * G + g) * D;
+    // One store per accumulator tile: 16 rows x 16 dims, 512 contiguous bytes.
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const f32x4 v = eng.o[rt][dt] * inv;
       uint2 packed;
       packed.x = pack_bf16x2(v[0], v[1]);
       packed.y = pack_bf16x2(v[2], v[3]);
-      *reinterpret_cast<uint2*>(po + dt * 16 + lg * 4) = packed;
+      *reinterpret_cast<uint2*>(a.parts.o + a.parts.o_index(D, h, chunk, m, dt * 16 + lg * 4)) =
+          packed;
     }
     if (lg == 0)
-      a.parts.lse[slot * G + g] = l_tot > 0.f ? eng.m_run[rt] + fast_log2(l_tot) : kNegInf;
+      a.parts.lse[a.parts.lse_index(h, chunk, m)] =
+          l_tot > 0.f ? eng.m_run[rt] + fast_log2(l_tot) : kNegInf;
   }
 }
 
@@ -290,16 +293,17 @@ __device__ __forceinline__ void decode_suffix_item(const DecodeArgs& a, int item
         pw[i] = pack_bf16x2(acc[g][2 * i] * inv, acc[g][2 * i + 1] * inv);
     }
   } else {
-    const int64_t slot =
-        ((int64_t)b * a.num_kv_heads + h) * a.parts.n_parts + a.parts.n_chunks + split;
+    const int j = a.parts.n_chunks + split;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
-      uint32_t* pw = reinterpret_cast<uint32_t*>(a.parts.o + (slot * G + g) * D + l16 * E);
+      const int row = b * G + g;
 #pragma unroll
       for (int i = 0; i < E / 2; ++i)
-        pw[i] = pack_bf16x2(acc[g][2 * i] * inv, acc[g][2 * i + 1] * inv);
-      if (l16 == 0) a.parts.lse[slot * G + g] = l[g] > 0.f ? m[g] + fast_log2(l[g]) : kNegInf;
+        *reinterpret_cast<uint32_t*>(a.parts.o + a.parts.o_index(D, h, j, row, l16 * E + 2 * i)) =
+            pack_bf16x2(acc[g][2 * i] * inv, acc[g][2 * i + 1] * inv);
+      if (l16 == 0)
+        a.parts.lse[a.parts.lse_index(h, j, row)] = l[g] > 0.f ? m[g] + fast_log2(l[g]) : kNegInf;
     }
   }
 }
@@ -312,6 +316,7 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
     decode_prefix_part<D>(lds, a, wg);
   } else {
     const int item = (wg - a.prefix_wgs) * (kEngineThreads / 64) + (threadIdx.x >> 6);
+    if (a.variant & 256) return;
     if (item < a.suffix_items) decode_suffix_item<D, G, suffix_tpg(D, G)>(a, item);
   }
 }
@@ -337,22 +342,29 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
   const int b = bh / a.num_kv_heads;
   const int h = bh - b * a.num_kv_heads;
   const int np = a.parts.n_parts;
-  const int64_t base = (int64_t)bh * np;
-  const uint2* po = reinterpret_cast<const uint2*>(a.parts.o + base * G * D);  // 4 bf16 per element
-  const float* pl = a.parts.lse + base * G;
   const int e = tid % E4;
   const int r = tid / E4;
   const bool active = r < R;
-  const int g = (e * 4) / D;
+  // Element e = 4 dims of one row: dims dt*16 + q4*4 .. +3 of head g, so
+  // consecutive threads read the G adjacent rows of one 16-dim tile.
+  const int q4 = e & 3;
+  const int g = (e >> 2) % G;
+  const int dt = e / (4 * G);
+  const int d = dt * 16 + q4 * 4;
+  const int row = b * G + g;
+  const int64_t part_stride = (int64_t)(D / 16) * a.parts.rows * 16;  // elements per part
+  const uint2* po =
+      reinterpret_cast<const uint2*>(a.parts.o + a.parts.o_index(D, h, 0, row, d));
 
   // Issue this thread's o loads first (independent of the weights).
   uint2 v[kCombineBatch];
 #pragma unroll
   for (int k = 0; k < kCombineBatch; ++k) {
     const int j = r + k * R;
-    v[k] = (active && j < np) ? po[(int64_t)j * E4 + e] : make_uint2(0, 0);
+    v[k] = (active && j < np) ? po[(int64_t)j * part_stride / 4] : make_uint2(0, 0);
   }
-  for (int i = tid; i < np * G; i += kCombineThreads) lse_s[i] = pl[i];
+  for (int i = tid; i < np * G; i += kCombineThreads)
+    lse_s[i] = a.parts.lse[a.parts.lse_index(h, i / G, b * G + i % G)];
   __syncthreads();
   if (tid < G) {
     float mx = kNegInf;
@@ -381,7 +393,7 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
 #pragma unroll
       for (int k = 0; k < kCombineBatch; ++k) {
         const int j = j0 + k * R;
-        v[k] = j < np ? po[(int64_t)j * E4 + e] : make_uint2(0, 0);
+        v[k] = j < np ? po[(int64_t)j * part_stride / 4] : make_uint2(0, 0);
       }
 #pragma unroll
       for (int k = 0; k < kCombineBatch; ++k) {
@@ -399,7 +411,6 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
   if (active && r == 0) {
     const float den = den_s[g];
     const f32x4 res = den > 0.f ? acc * (1.f / den) : f32x4{0.f, 0.f, 0.f, 0.f};
-    const int d = e * 4 - g * D;
     uint2 packed;
     packed.x = pack_bf16x2(res[0], res[1]);
     packed.y = pack_bf16x2(res[2], res[3]);

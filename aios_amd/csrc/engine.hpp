@@ -94,6 +94,7 @@ struct TileEngine {
   float l_run[2];
   int limit[2];    // CAUSAL: last visible KV position of the lane's rows
   int min_limit;   // CAUSAL: smallest limit of any row of the workgroup
+  int abl = 0;     // timing ablations (experiments only)
 
   // Q fragment (B operand of S^T = K Q^T) of the lane's two rows.
   __device__ __forceinline__ void load_q(const bf16* q0, bool ok0, const bf16* q1, bool ok1) {
@@ -251,6 +252,7 @@ struct TileEngine {
       st[0][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
       st[1][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    if (!(abl & 4)) {
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
@@ -258,6 +260,10 @@ struct TileEngine {
         st[0][tt] = mfma16x16x32(kf[tt][s], qf[0][s], st[0][tt]);
         st[1][tt] = mfma16x16x32(kf[tt][s], qf[1][s], st[1][tt]);
       }
+    } else {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) { st[0][tt] += __builtin_bit_cast(f32x4, kf[tt][0]); }
+    }
 
     // Online softmax with a lazily moved reference: m_run only moves when a
     // row's scaled max exceeds it by more than kRescaleSlack (p <= 2^slack
@@ -326,6 +332,12 @@ struct TileEngine {
     // O^T += V^T P^T.  Lane (lg, l16) supplied V[token][dt*16 + 4*(l16%4)..+3]
     // of tokens lg*4 + l16/4 (first read) and 16 + lg*4 + l16/4 (second read)
     // and received V[tokens][dt*16 + l16], the A fragment rows of the MFMA.
+    if (abl & 1) {
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt)
+        o[0][dt] += __builtin_bit_cast(f32x4, __builtin_shufflevector(va[dt][0], va[dt][1], 0, 1, 2, 3, 4, 5, 6, 7)) + __builtin_bit_cast(f32x4, pb[dt & 1]);
+      return;
+    }
 #pragma unroll
     for (int dt = 0; dt < DTILES; ++dt) {
       const bf16x8 vf = __builtin_shufflevector(va[dt][0], va[dt][1], 0, 1, 2, 3, 4, 5, 6, 7);

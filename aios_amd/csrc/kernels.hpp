@@ -6,16 +6,27 @@
 
 namespace aios {
 
-// Partial softmax states of a decode batch live in one workspace array,
-// contiguous per (row b, kv-head h):
-//   parts_o  [B][Hkv][n_parts][G][D] bf16 (normalised o = acc / l)
-//   parts_lse[B][Hkv][n_parts][G]    fp32 (log2-domain m + log2 l; -inf = empty)
-// Slot j < n_chunks holds prefix chunk j; slot n_chunks + s holds suffix split s.
+// Partial softmax states of a decode batch live in one workspace array.
+// Rows are the batch * G query rows m = b * G + g; for kv-head h and part j
+// (slot j < n_chunks: prefix chunk j; n_chunks + s: suffix split s):
+//   o   [Hkv][n_parts][D/16][rows][16] bf16 (normalised o = acc / l)
+//   lse [Hkv][n_parts][rows]           fp32 (log2-domain m + log2 l; -inf = empty)
+// so the 16 rows x 16 dims an MFMA accumulator tile holds are one
+// contiguous 512-byte run, and the G rows of one (b, h, j) are adjacent.
 struct PartsArgs {
   bf16* o;
   float* lse;
   int32_t n_parts;
   int32_t n_chunks;
+  int32_t rows;  // batch * G
+
+  // Element (h, j, m, d) of o for head dimension D.
+  __host__ __device__ int64_t o_index(int D, int h, int j, int m, int d) const {
+    return ((((int64_t)h * n_parts + j) * (D >> 4) + (d >> 4)) * rows + m) * 16 + (d & 15);
+  }
+  __host__ __device__ int64_t lse_index(int h, int j, int m) const {
+    return ((int64_t)h * n_parts + j) * rows + m;
+  }
 };
 
 struct DecodeArgs {

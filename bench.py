@@ -287,7 +287,12 @@ def main() -> int:
     casc_ms = per_launch_ms(main_calls, max(2, args.steps // 4))
     comb_ms = per_launch_ms(comb_calls, max(2, args.steps // 4))
 
-    # Untimed check of the last step against a split-free recomputation.
+    # Untimed check of one full step against a recomputation without the
+    # shared-prefix cascade (the per-launch timing above reuses the workspace
+    # across layers, so the step is run again first).
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.synchronize()
     plan_all = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=0)
     ws2 = torch.empty(max(plan_all.ws_bytes, 256), dtype=torch.uint8, device=dev)
     ref0 = paged.decode(plan_all, wl.q[0], wl.k_cache[0], wl.v_cache[0], indices, cu_k, workspace=ws2)
