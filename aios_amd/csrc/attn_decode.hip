@@ -24,45 +24,6 @@
 
 namespace aios {
 
-template <int E>
-struct Slice {
-  uint32_t w[E / 2];
-};
-
-template <int E>
-__device__ __forceinline__ Slice<E> load_slice(const bf16* p) {
-  Slice<E> r;
-  if constexpr (E == 8) {
-    const uint4 v = *reinterpret_cast<const uint4*>(p);
-    r.w[0] = v.x;
-    r.w[1] = v.y;
-    r.w[2] = v.z;
-    r.w[3] = v.w;
-  } else if constexpr (E == 4) {
-    const uint2 v = *reinterpret_cast<const uint2*>(p);
-    r.w[0] = v.x;
-    r.w[1] = v.y;
-  } else {
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-#pragma unroll
-    for (int i = 0; i < E / 2; ++i) r.w[i] = q[i];
-  }
-  return r;
-}
-
-template <int E>
-__device__ __forceinline__ void store_slice(bf16* p, const Slice<E>& s) {
-  if constexpr (E == 8) {
-    *reinterpret_cast<uint4*>(p) = make_uint4(s.w[0], s.w[1], s.w[2], s.w[3]);
-  } else if constexpr (E == 4) {
-    *reinterpret_cast<uint2*>(p) = make_uint2(s.w[0], s.w[1]);
-  } else {
-    uint32_t* q = reinterpret_cast<uint32_t*>(p);
-#pragma unroll
-    for (int i = 0; i < E / 2; ++i) q[i] = s.w[i];
-  }
-}
-
 // ---------------------------------------------------------------------------
 // prefix part
 template <int D>
@@ -83,7 +44,6 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
 
   TileEngine<D, false> eng;
   eng.min_limit = 0x7fffffff;
-  eng.abl = a.variant >> 4;
   int rows[2];
   bool ok[2];
   const bf16* qr[2];
@@ -107,7 +67,6 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
           [&] { eng.load_q(qr[0], ok[0], qr[1], ok[1]); }, active);
 
   constexpr int DT = D / 16;
-  if (a.variant & 128) return;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const float l_tot = eng.l_run[rt];
@@ -133,10 +92,17 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
 }
 
 // ---------------------------------------------------------------------------
-// suffix part: one wavefront per (row, kv-head, split) item
-template <int D, int G, int TPG>
-__device__ __forceinline__ void decode_suffix_item(const DecodeArgs& a, int item) {
-  constexpr int E = D / 16;
+// suffix part: one wavefront per (row, kv-head, split) item.  The wavefront
+// gathers 32 positions at a time of the row's own pages into its own LDS
+// sub-tile (the engine's layout) and runs the engine math with one 16-row
+// MFMA tile whose first G rows are the row's query heads.
+template <int D, int G>
+__device__ __forceinline__ void decode_suffix_item(uint8_t* buf, const DecodeArgs& a, int item) {
+  using T = KVTile<D>;
+  constexpr int CH = T::SUB_BYTES / 16;  // 16-byte chunks per sub-tile (K then V)
+  constexpr int NJ = CH / 64;            // DMA loads per lane per sub-tile
+  static_assert(CH % 64 == 0, "sub-tile must split over one wavefront");
+  static_assert(G <= 16, "one MFMA row tile");
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15;
   const int lg = lane >> 4;
@@ -150,162 +116,93 @@ __device__ __forceinline__ void decode_suffix_item(const DecodeArgs& a, int item
   const int s_begin = a.prefix_len + split * a.split_len;
   const int s_end = min(kv_len, s_begin + a.split_len);
 
-  float q[G][E];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const Slice<E> qs =
-        load_slice<E>(a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + g) * D + l16 * E);
-#pragma unroll
-    for (int i = 0; i < E / 2; ++i) {
-      q[g][2 * i] = lo_bf16(qs.w[i]);
-      q[g][2 * i + 1] = hi_bf16(qs.w[i]);
-    }
-  }
+  TileEngine<D, false, 1> eng;
+  eng.reset();
+  eng.load_q_tile(0, a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + min(l16, G - 1)) * D,
+                  l16 < G);
 
-  float m[G], l[G], acc[G][E];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = kNegInf;
-    l[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
-  }
-
-  const bf16* kb = a.k_cache + (int64_t)h * D + l16 * E;
-  const bf16* vb = a.v_cache + (int64_t)h * D + l16 * E;
-  // Fused append: the row's last position is its new token, taken from
-  // k_new / v_new and written to its page here (no other workgroup of the
-  // launch reads that page).
+  // Fused append: the row's last position is its new token, gathered from
+  // k_new / v_new (page selector kNewTok) and written to its page below (no
+  // other workgroup of the launch reads that page).
+  constexpr uint32_t kNoPage = 0xffffffffu;
+  constexpr uint32_t kNewTok = 0xfffffffeu;
   const int t_new = a.k_new != nullptr ? kv_len - 1 : -1;
-  for (int t0 = s_begin; t0 < s_end; t0 += 4 * TPG) {
-    int64_t page[TPG];
+  // A slot outside the pool is not written, and the row then attends to
+  // zeros there, as the separate append and decode would.
+  const int64_t new_dst = a.k_new != nullptr ? (int64_t)a.out_loc[b] : -1;
+  const bool new_ok = (uint64_t)new_dst < (uint64_t)a.num_pages;
+  const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2;
+  const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2;
+  const uint8_t* kn = a.k_new != nullptr
+                          ? reinterpret_cast<const uint8_t*>(a.k_new + (int64_t)b * a.k_new_stride +
+                                                             (int64_t)h * D)
+                          : g_zero_kv_row;
+  const uint8_t* vn = a.k_new != nullptr
+                          ? reinterpret_cast<const uint8_t*>(a.v_new + (int64_t)b * a.v_new_stride +
+                                                             (int64_t)h * D)
+                          : g_zero_kv_row;
+  const uint32_t tok_b = (uint32_t)(a.kv_tok_stride * 2);
+  const uint32_t n_pages = (uint32_t)a.num_pages;
+  int tok_j[NJ];
+  uint32_t coff_j[NJ];
+  bool isv_j[NJ];
 #pragma unroll
-    for (int u = 0; u < TPG; ++u) {
-      const int t = t0 + 4 * u + lg;
-      page[u] = t < s_end ? (int64_t)a.indices[base + t] : -1;
+  for (int j = 0; j < NJ; ++j) {
+    const int c = j * 64 + lane;
+    const bool isv = c >= CH / 2;
+    const int c2 = isv ? c - CH / 2 : c;
+    const int t = c2 / T::CPR;
+    const int slot = c2 - t * T::CPR;
+    tok_j[j] = t;
+    isv_j[j] = isv;
+    coff_j[j] = (uint32_t)((isv ? T::v_chunk(t, slot) : T::k_chunk(t, slot)) * 16);
+  }
+  for (int kv0 = s_begin; kv0 < s_end; kv0 += kSubTok) {
+    const int pos = kv0 + lane;
+    uint32_t sel = kNoPage;
+    if (lane < kSubTok && pos < s_end)
+      sel = pos == t_new ? (new_ok ? kNewTok : kNoPage) : (uint32_t)a.indices[base + pos];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t page = (uint32_t)__shfl((int)sel, tok_j[j]);
+      const uint8_t* src = page < n_pages ? (isv_j[j] ? vc : kc) + (page * tok_b + coff_j[j])
+                           : page == kNewTok ? (isv_j[j] ? vn : kn) + coff_j[j]
+                                             : g_zero_kv_row + coff_j[j];
+      __builtin_amdgcn_global_load_lds(src, (AIOS_LDS void*)(buf + j * 64 * 16), 16, 0, 0);
     }
-    Slice<E> ks[TPG], vs[TPG];
-#pragma unroll
-    for (int u = 0; u < TPG; ++u) {
-      if (t0 + 4 * u + lg == t_new) {
-        ks[u] = load_slice<E>(a.k_new + (int64_t)b * a.k_new_stride + (int64_t)h * D + l16 * E);
-        vs[u] = load_slice<E>(a.v_new + (int64_t)b * a.v_new_stride + (int64_t)h * D + l16 * E);
-      } else if ((uint64_t)page[u] < (uint64_t)a.num_pages) {
-        ks[u] = load_slice<E>(kb + page[u] * a.kv_tok_stride);
-        vs[u] = load_slice<E>(vb + page[u] * a.kv_tok_stride);
-      } else {
-#pragma unroll
-        for (int i = 0; i < E / 2; ++i) ks[u].w[i] = vs[u].w[i] = 0u;
-      }
-    }
-    if (t_new >= t0 && t_new < t0 + 4 * TPG && (t_new - t0) % 4 == lg) {
-      const int u = (t_new - t0) / 4;
-      const int64_t dst = a.out_loc[b];
-      if ((uint64_t)dst < (uint64_t)a.num_pages) {
-        const int64_t off = dst * a.kv_tok_stride + (int64_t)h * D + l16 * E;
-#pragma unroll
-        for (int uu = 0; uu < TPG; ++uu) {
-          if (uu == u) {
-            store_slice<E>(const_cast<bf16*>(a.k_cache) + off, ks[uu]);
-            store_slice<E>(const_cast<bf16*>(a.v_cache) + off, vs[uu]);
-          }
-        }
-      } else {
-        // The separate append would skip this row and the decode would read
-        // page out_loc[b] as zeros.
-#pragma unroll
-        for (int uu = 0; uu < TPG; ++uu) {
-          if (uu == u) {
-#pragma unroll
-            for (int i = 0; i < E / 2; ++i) ks[uu].w[i] = vs[uu].w[i] = 0u;
-          }
-        }
-      }
-    }
-    float sc[TPG][G];
-#pragma unroll
-    for (int u = 0; u < TPG; ++u) {
-      const bool ok = t0 + 4 * u + lg < s_end;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int i = 0; i < E / 2; ++i) {
-          d = fmaf(q[g][2 * i], lo_bf16(ks[u].w[i]), d);
-          d = fmaf(q[g][2 * i + 1], hi_bf16(ks[u].w[i]), d);
-        }
-        d = row16_sum(d);
-        sc[u][g] = ok ? d * a.scale_log2 : kNegInf;
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mx = sc[0][g];
-#pragma unroll
-      for (int u = 1; u < TPG; ++u) mx = fmaxf(mx, sc[u][g]);
-      const float m_new = fmaxf(m[g], mx);
-      const float mu = (m_new == kNegInf) ? 0.f : m_new;
-      const float alpha = fast_exp2(m[g] - mu);
-      float p[TPG];
-      float ps = 0.f;
-#pragma unroll
-      for (int u = 0; u < TPG; ++u) {
-        p[u] = fast_exp2(sc[u][g] - mu);
-        ps += p[u];
-      }
-      l[g] = l[g] * alpha + ps;
-#pragma unroll
-      for (int i = 0; i < E / 2; ++i) {
-        float a0 = acc[g][2 * i] * alpha;
-        float a1 = acc[g][2 * i + 1] * alpha;
-#pragma unroll
-        for (int u = 0; u < TPG; ++u) {
-          a0 = fmaf(p[u], lo_bf16(vs[u].w[i]), a0);
-          a1 = fmaf(p[u], hi_bf16(vs[u].w[i]), a1);
-        }
-        acc[g][2 * i] = a0;
-        acc[g][2 * i + 1] = a1;
-      }
-      m[g] = m_new;
-    }
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    eng.compute(buf, kv0, s_end, a.scale_log2, l16, lg);
+  }
+  eng.finish();
+
+  if (new_ok && t_new >= s_begin && t_new < s_end && lane < 2 * T::CPR) {
+    const bool isv = lane >= T::CPR;
+    const int c = isv ? lane - T::CPR : lane;
+    const uint4 v = *reinterpret_cast<const uint4*>((isv ? vn : kn) + c * 16);
+    *reinterpret_cast<uint4*>(const_cast<uint8_t*>(isv ? vc : kc) + new_dst * tok_b + c * 16) = v;
   }
 
-  // Merge the four DPP rows.
+  if (l16 >= G) return;
+  constexpr int DT = D / 16;
+  const float l_tot = eng.l_run[0];
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const int row = b * G + l16;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float mx = xrow_max(m[g]);
-    const float mu = (mx == kNegInf) ? 0.f : mx;
-    const float f = fast_exp2(m[g] - mu);
-    l[g] = xrow_sum(l[g] * f);
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[g][e] = xrow_sum(acc[g][e] * f);
-    m[g] = mx;
+  for (int dt = 0; dt < DT; ++dt) {
+    const f32x4 v = eng.o[0][dt] * inv;
+    uint2 packed;
+    packed.x = pack_bf16x2(v[0], v[1]);
+    packed.y = pack_bf16x2(v[2], v[3]);
+    bf16* dstp = a.final_out
+                     ? a.out + ((int64_t)b * a.num_qo_heads + h * G + l16) * D + dt * 16 + lg * 4
+                     : a.parts.o + a.parts.o_index(D, h, a.parts.n_chunks + split, row,
+                                                   dt * 16 + lg * 4);
+    *reinterpret_cast<uint2*>(dstp) = packed;
   }
-  if (lg != 0) return;
-  if (a.final_out) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
-      uint32_t* pw = reinterpret_cast<uint32_t*>(
-          a.out + ((int64_t)b * a.num_qo_heads + h * G + g) * D + l16 * E);
-#pragma unroll
-      for (int i = 0; i < E / 2; ++i)
-        pw[i] = pack_bf16x2(acc[g][2 * i] * inv, acc[g][2 * i + 1] * inv);
-    }
-  } else {
-    const int j = a.parts.n_chunks + split;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
-      const int row = b * G + g;
-#pragma unroll
-      for (int i = 0; i < E / 2; ++i)
-        *reinterpret_cast<uint32_t*>(a.parts.o + a.parts.o_index(D, h, j, row, l16 * E + 2 * i)) =
-            pack_bf16x2(acc[g][2 * i] * inv, acc[g][2 * i + 1] * inv);
-      if (l16 == 0)
-        a.parts.lse[a.parts.lse_index(h, j, row)] = l[g] > 0.f ? m[g] + fast_log2(l[g]) : kNegInf;
-    }
-  }
+  if (!a.final_out && lg == 0)
+    a.parts.lse[a.parts.lse_index(h, a.parts.n_chunks + split, row)] =
+        l_tot > 0.f ? eng.m_run[0] + fast_log2(l_tot) : kNegInf;
 }
 
 template <int D, int G>
@@ -315,9 +212,10 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
   if (wg < a.prefix_wgs) {
     decode_prefix_part<D>(lds, a, wg);
   } else {
-    const int item = (wg - a.prefix_wgs) * (kEngineThreads / 64) + (threadIdx.x >> 6);
-    if (a.variant & 256) return;
-    if (item < a.suffix_items) decode_suffix_item<D, G, suffix_tpg(D, G)>(a, item);
+    const int wave = threadIdx.x >> 6;
+    const int item = (wg - a.prefix_wgs) * (kEngineThreads / 64) + wave;
+    if (item < a.suffix_items)
+      decode_suffix_item<D, G>(lds + wave * KVTile<D>::SUB_BYTES, a, item);
   }
 }
 

@@ -82,35 +82,48 @@ struct KVTile {
   }
 };
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, int RT = 2>
 struct TileEngine {
   using T = KVTile<D>;
   static constexpr int KSTEPS = D / 32;
   static constexpr int DTILES = D / 16;
 
-  bf16x8 qf[2][KSTEPS];
-  f32x4 o[2][DTILES];
-  float m_run[2];
-  float l_run[2];
-  int limit[2];    // CAUSAL: last visible KV position of the lane's rows
+  bf16x8 qf[RT][KSTEPS];
+  f32x4 o[RT][DTILES];
+  float m_run[RT];
+  float l_run[RT];
+  int limit[RT];   // CAUSAL: last visible KV position of the lane's rows
   int min_limit;   // CAUSAL: smallest limit of any row of the workgroup
-  int abl = 0;     // timing ablations (experiments only)
 
-  // Q fragment (B operand of S^T = K Q^T) of the lane's two rows.
-  __device__ __forceinline__ void load_q(const bf16* q0, bool ok0, const bf16* q1, bool ok1) {
+  // Q fragment (B operand of S^T = K Q^T) of the lane's row in tile rt.
+  __device__ __forceinline__ void load_q_tile(int rt, const bf16* q, bool ok) {
     const int lg = (threadIdx.x & 63) >> 4;
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      qf[0][s] = ok0 ? *reinterpret_cast<const bf16x8*>(q0 + s * 32 + lg * 8) : bf16x8{};
-      qf[1][s] = ok1 ? *reinterpret_cast<const bf16x8*>(q1 + s * 32 + lg * 8) : bf16x8{};
+    for (int s = 0; s < KSTEPS; ++s)
+      qf[rt][s] = ok ? *reinterpret_cast<const bf16x8*>(q + s * 32 + lg * 8) : bf16x8{};
+  }
+  __device__ __forceinline__ void load_q(const bf16* q0, bool ok0, const bf16* q1, bool ok1) {
+    static_assert(RT == 2, "two row tiles");
+    load_q_tile(0, q0, ok0);
+    load_q_tile(1, q1, ok1);
+  }
+
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_run[rt] = kNegInf;
+      l_run[rt] = 0.f;
     }
   }
 
   // Stream KV positions [kv_begin, kv_end) of one kv-head (kc / vc point at
   // head h of page 0; tok_bytes = page stride) whose page ids are
-  // idx[kv_begin .. kv_end).  `qload` loads the Q fragment; an inactive
-  // wavefront (all of its rows padding) streams K/V but skips the math.
-  // Leaves o (unnormalised), m_run and the row total l_run.
+  // idx[kv_begin .. kv_end), with all kEngineThreads threads of the
+  // workgroup.  `qload` loads the Q fragment; an inactive wavefront (all of
+  // its rows padding) streams K/V but skips the math.  Leaves o
+  // (unnormalised), m_run and the row total l_run.
   template <typename QLoad>
   __device__ void run(uint8_t* lds, const uint8_t* kc, const uint8_t* vc, int64_t tok_bytes,
                       int64_t num_pages, const int32_t* idx, int kv_begin, int kv_end,
@@ -120,13 +133,7 @@ struct TileEngine {
     const int wave = tid >> 6;
     const int l16 = lane & 15;
     const int lg = lane >> 4;
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-#pragma unroll
-      for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      m_run[rt] = kNegInf;
-      l_run[rt] = 0.f;
-    }
+    reset();
     const int n_sub = (kv_end - kv_begin + kSubTok - 1) / kSubTok;
     if (n_sub <= 0) return;
 
@@ -207,10 +214,17 @@ struct TileEngine {
         compute(lds + (it & (kRing - 1)) * T::SUB_BYTES, kv_begin + it * kSubTok, kv_end,
                 scale_log2, l16, lg);
     }
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) l_run[rt] = xrow_sum(l_run[rt]);
+    finish();
   }
 
+  // Row totals across the four lane groups (after the last compute).
+  __device__ __forceinline__ void finish() {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) l_run[rt] = xrow_sum(l_run[rt]);
+  }
+
+  // One 32-token sub-tile in LDS (KVTile layout) for the lane's RT rows;
+  // positions >= kv_end (and, if CAUSAL, past each row's limit) are masked.
   __device__ __forceinline__ void compute(const uint8_t* kb, int kv0, int kv_end, float scale_log2,
                                           int l16, int lg) {
     const uint8_t* vb = kb + T::SUB_KB;
@@ -245,34 +259,28 @@ struct TileEngine {
       }
     }
     // S^T tiles: st[rt][tt][i] = S[row rt*16 + l16][token tt*16 + lg*4 + i];
-    // the four accumulation chains are interleaved.
-    f32x4 st[2][2];
+    // the accumulation chains are interleaved.
+    f32x4 st[RT][2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      st[0][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      st[1][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    if (!(abl & 4)) {
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) st[rt][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        st[0][tt] = mfma16x16x32(kf[tt][s], qf[0][s], st[0][tt]);
-        st[1][tt] = mfma16x16x32(kf[tt][s], qf[1][s], st[1][tt]);
-      }
-    } else {
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) { st[0][tt] += __builtin_bit_cast(f32x4, kf[tt][0]); }
-    }
+        for (int rt = 0; rt < RT; ++rt)
+          st[rt][tt] = mfma16x16x32(kf[tt][s], qf[rt][s], st[rt][tt]);
 
     // Online softmax with a lazily moved reference: m_run only moves when a
     // row's scaled max exceeds it by more than kRescaleSlack (p <= 2^slack
     // otherwise), so the O rescale below is skipped once the max settles.
     const bool full = kv0 + kSubTok <= kv_end && (!CAUSAL || kv0 + kSubTok - 1 <= min_limit);
-    float x[2][8];
-    float mx[2];
+    float x[RT][8];
+    float mx[RT];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -291,30 +299,29 @@ struct TileEngine {
       mx[rt] = fmaxf(fmaxf(fmaxf(x[rt][0], x[rt][1]), fmaxf(x[rt][2], x[rt][3])),
                      fmaxf(fmaxf(x[rt][4], x[rt][5]), fmaxf(x[rt][6], x[rt][7])));
     }
-    mx[0] = xrow_max(mx[0]) * scale_log2;
-    mx[1] = xrow_max(mx[1]) * scale_log2;
-    const bool need0 = mx[0] > m_run[0] + kRescaleSlack;
-    const bool need1 = mx[1] > m_run[1] + kRescaleSlack;
-    if (__builtin_amdgcn_ballot_w64(need0 || need1)) {
+    bool need[RT];
+    bool any = false;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      mx[rt] = xrow_max(mx[rt]) * scale_log2;
+      need[rt] = mx[rt] > m_run[rt] + kRescaleSlack;
+      any = any || need[rt];
+    }
+    if (__builtin_amdgcn_ballot_w64(any)) {
       // Rows that keep their reference use alpha = 1 exactly (their reference
       // may still be -inf); a moved reference from -inf gives alpha = 0.
-      const float a0 = need0 ? fast_exp2(m_run[0] - mx[0]) : 1.f;
-      const float a1 = need1 ? fast_exp2(m_run[1] - mx[1]) : 1.f;
-      const float mn0 = need0 ? mx[0] : m_run[0];
-      const float mn1 = need1 ? mx[1] : m_run[1];
-      l_run[0] *= a0;
-      l_run[1] *= a1;
 #pragma unroll
-      for (int dt = 0; dt < DTILES; ++dt) {
-        o[0][dt] *= a0;
-        o[1][dt] *= a1;
+      for (int rt = 0; rt < RT; ++rt) {
+        const float al = need[rt] ? fast_exp2(m_run[rt] - mx[rt]) : 1.f;
+        l_run[rt] *= al;
+#pragma unroll
+        for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] *= al;
+        m_run[rt] = need[rt] ? mx[rt] : m_run[rt];
       }
-      m_run[0] = mn0;
-      m_run[1] = mn1;
     }
-    bf16x8 pb[2];
+    bf16x8 pb[RT];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const float m_use = (m_run[rt] == kNegInf) ? 0.f : m_run[rt];
       float p[8];
       float psum = 0.f;
@@ -332,17 +339,11 @@ struct TileEngine {
     // O^T += V^T P^T.  Lane (lg, l16) supplied V[token][dt*16 + 4*(l16%4)..+3]
     // of tokens lg*4 + l16/4 (first read) and 16 + lg*4 + l16/4 (second read)
     // and received V[tokens][dt*16 + l16], the A fragment rows of the MFMA.
-    if (abl & 1) {
-#pragma unroll
-      for (int dt = 0; dt < DTILES; ++dt)
-        o[0][dt] += __builtin_bit_cast(f32x4, __builtin_shufflevector(va[dt][0], va[dt][1], 0, 1, 2, 3, 4, 5, 6, 7)) + __builtin_bit_cast(f32x4, pb[dt & 1]);
-      return;
-    }
 #pragma unroll
     for (int dt = 0; dt < DTILES; ++dt) {
       const bf16x8 vf = __builtin_shufflevector(va[dt][0], va[dt][1], 0, 1, 2, 3, 4, 5, 6, 7);
-      o[0][dt] = mfma16x16x32(vf, pb[0], o[0][dt]);
-      o[1][dt] = mfma16x16x32(vf, pb[1], o[1][dt]);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) o[rt][dt] = mfma16x16x32(vf, pb[rt], o[rt][dt]);
     }
   }
 };

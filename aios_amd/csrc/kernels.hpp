@@ -98,14 +98,11 @@ hipError_t greedy_select(const void* logits, int64_t row_stride, int32_t rows, i
                          int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                          hipStream_t stream);
 
-// KV positions each 16-lane DPP row of a suffix wavefront holds per pass
-// (4 * tpg positions per pass), sized so the K/V slices fit the registers.
-__host__ __device__ constexpr int suffix_tpg(int D, int G) {
-  return G * D <= 384 ? 16 : (G * D <= 512 ? 8 : 4);
-}
+// KV positions a suffix wavefront gathers per pass (one engine sub-tile).
+constexpr int kSuffixPass = 32;
 
 // One launch: prefix-chunk workgroups (MFMA tile engine) followed by suffix
-// workgroups (eight (row, head, split) items per workgroup).
+// workgroups (four (row, head, split) items per workgroup, one per wavefront).
 hipError_t launch_decode_main(int D, const DecodeArgs& a, hipStream_t stream);
 
 // Log-sum-exp merge of every part of each (row, kv-head) into bf16 out.
