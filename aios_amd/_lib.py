@@ -30,6 +30,9 @@ EXPORTED_SYMBOLS = (
     "aios_attn_decode",
     "aios_attn_append_decode",
     "aios_build_indices",
+    "aios_rmsnorm",
+    "aios_qk_norm_rope",
+    "aios_silu_mul",
     "aios_greedy_select",
 )
 
@@ -109,6 +112,13 @@ def _declare(lib: ctypes.CDLL) -> None:
     ]
     lib.aios_build_indices.restype = ctypes.c_int
     lib.aios_build_indices.argtypes = [_vp, _i64, _vp, _vp, _i32, _i32, _vp, _vp]
+    lib.aios_rmsnorm.restype = ctypes.c_int
+    lib.aios_rmsnorm.argtypes = [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i32, _f32, _vp]
+    lib.aios_qk_norm_rope.restype = ctypes.c_int
+    lib.aios_qk_norm_rope.argtypes = [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64,
+                                      _vp, _vp, _vp, _f32, _vp]
+    lib.aios_silu_mul.restype = ctypes.c_int
+    lib.aios_silu_mul.argtypes = [_vp, _i64, _i64, _i32, _vp, _i64, _vp]
     lib.aios_greedy_select.restype = ctypes.c_int
     lib.aios_greedy_select.argtypes = [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]
 

@@ -381,6 +381,63 @@ int aios_build_indices(const int32_t* page_table, int64_t page_table_stride,
                    "build_indices launch");
 }
 
+int aios_rmsnorm(const void* x, int64_t x_stride, void* residual, int64_t residual_stride,
+                 const void* weight, void* out, int64_t out_stride, int64_t rows, int32_t hidden,
+                 float eps, void* stream) {
+  if (rows < 0 || !aios::rmsnorm_supported(hidden))
+    return fail(AIOS_ERR_INVALID, "rmsnorm: hidden %d must be a multiple of 8 up to 8192", hidden);
+  if (rows == 0) return AIOS_OK;
+  if (!x || !weight || !out) return fail(AIOS_ERR_INVALID, "rmsnorm: null pointer");
+  if (x_stride < hidden || out_stride < hidden || (residual && residual_stride < hidden) ||
+      (x_stride | out_stride | (residual ? residual_stride : 0)) % 8 != 0)
+    return fail(AIOS_ERR_INVALID, "rmsnorm: row strides must be >= hidden and multiples of 8");
+  if ((((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)residual) & 15) != 0)
+    return fail(AIOS_ERR_INVALID, "rmsnorm: rows must be 16-byte aligned");
+  return check_hip(aios::rmsnorm(x, x_stride, residual, residual_stride, weight, out, out_stride,
+                                 rows, hidden, eps, static_cast<hipStream_t>(stream)),
+                   "rmsnorm launch");
+}
+
+int aios_qk_norm_rope(const void* qkv, int64_t qkv_stride, int64_t tokens, int32_t num_qo_heads,
+                      int32_t num_kv_heads, int32_t head_dim, const void* q_weight,
+                      const void* k_weight, const float* cos_table, const float* sin_table,
+                      int64_t table_rows, const int32_t* positions, void* q_out, void* k_out,
+                      float eps, void* stream) {
+  if (tokens < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || table_rows <= 0)
+    return fail(AIOS_ERR_INVALID, "qk_norm_rope: bad sizes");
+  if (!aios::head_dim_supported(head_dim))
+    return fail(AIOS_ERR_UNSUPPORTED, "qk_norm_rope: head_dim %d is not built", head_dim);
+  if (qkv_stride < (int64_t)(num_qo_heads + 2 * num_kv_heads) * head_dim || qkv_stride % 2 != 0)
+    return fail(AIOS_ERR_INVALID, "qk_norm_rope: qkv row stride too small");
+  if (tokens == 0) return AIOS_OK;
+  if (!qkv || !q_weight || !k_weight || !cos_table || !sin_table || !positions || !q_out || !k_out)
+    return fail(AIOS_ERR_INVALID, "qk_norm_rope: null pointer");
+  if ((((uintptr_t)qkv | (uintptr_t)q_weight | (uintptr_t)k_weight) & 3) != 0)
+    return fail(AIOS_ERR_INVALID, "qk_norm_rope: rows must be 4-byte aligned");
+  return check_hip(aios::qk_norm_rope(qkv, qkv_stride, tokens, num_qo_heads, num_kv_heads, head_dim,
+                                      q_weight, k_weight, cos_table, sin_table, table_rows,
+                                      positions, q_out, k_out, eps,
+                                      static_cast<hipStream_t>(stream)),
+                   "qk_norm_rope launch");
+}
+
+int aios_silu_mul(const void* x, int64_t x_stride, int64_t rows, int32_t intermediate, void* out,
+                  int64_t out_stride, void* stream) {
+  if (rows < 0 || intermediate <= 0 || intermediate % 8 != 0)
+    return fail(AIOS_ERR_INVALID, "silu_mul: intermediate size %d must be a multiple of 8",
+                intermediate);
+  if (x_stride < 2 * (int64_t)intermediate || out_stride < intermediate ||
+      (x_stride | out_stride) % 8 != 0)
+    return fail(AIOS_ERR_INVALID, "silu_mul: row strides too small or not multiples of 8");
+  if (rows == 0) return AIOS_OK;
+  if (!x || !out) return fail(AIOS_ERR_INVALID, "silu_mul: null pointer");
+  if ((((uintptr_t)x | (uintptr_t)out) & 15) != 0)
+    return fail(AIOS_ERR_INVALID, "silu_mul: rows must be 16-byte aligned");
+  return check_hip(aios::silu_mul(x, x_stride, rows, intermediate, out, out_stride,
+                                  static_cast<hipStream_t>(stream)),
+                   "silu_mul launch");
+}
+
 int aios_greedy_select(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
                        int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                        void* stream) {

@@ -94,6 +94,19 @@ hipError_t build_indices(const int32_t* page_table, int64_t pt_stride, const int
                          const int32_t* cu_k, int32_t batch, int32_t max_len,
                          int32_t* indices, hipStream_t stream);
 
+hipError_t rmsnorm(const void* x, int64_t x_stride, void* residual, int64_t r_stride,
+                   const void* w, void* out, int64_t out_stride, int64_t rows, int hidden,
+                   float eps, hipStream_t stream);
+bool rmsnorm_supported(int hidden);
+
+hipError_t qk_norm_rope(const void* qkv, int64_t stride, int64_t tokens, int hq, int hkv, int D,
+                        const void* qw, const void* kw, const float* cos_t, const float* sin_t,
+                        int64_t table_rows, const int32_t* positions, void* q_out, void* k_out,
+                        float eps, hipStream_t stream);
+
+hipError_t silu_mul(const void* x, int64_t x_stride, int64_t rows, int inter, void* out,
+                    int64_t out_stride, hipStream_t stream);
+
 hipError_t greedy_select(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
                          int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                          hipStream_t stream);

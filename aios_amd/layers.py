@@ -1,0 +1,80 @@
+"""Decoder-layer ops on the gfx950 kernels (the layers the reference takes
+from FlashInfer and torch: python/aios/layers/norm.py:10-40,
+layers/activation.py:9-12, layers/attention.py:11-16 and the q/k norm of
+models/qwen3.py:65-66).
+
+``HipOps`` is the op set the decoder uses on the GPU; every call goes
+through the C ABI of libaios_attn.so and fails loudly without it.
+"""
+from __future__ import annotations
+
+import torch
+
+from aios_amd import _lib
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check_rows(t: torch.Tensor, name: str) -> None:
+    if t.dtype != torch.bfloat16 or not t.is_cuda or t.ndim != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D bfloat16 GPU tensor with contiguous rows")
+
+
+class HipOps:
+    """RMSNorm, residual-add RMSNorm, q/k RMSNorm + RoPE, SiLU-and-mul."""
+
+    @staticmethod
+    def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+        _check_rows(x, "x")
+        out = torch.empty_like(x)
+        _lib.check(_lib.lib().aios_rmsnorm(x.data_ptr(), x.stride(0), None, 0, weight.data_ptr(),
+                                           out.data_ptr(), out.stride(0), x.shape[0], x.shape[1],
+                                           eps, _stream(x)), "aios_rmsnorm")
+        return out
+
+    @staticmethod
+    def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                          eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+        """residual <- x + residual; x <- RMSNorm(residual) * weight (both in place)."""
+        _check_rows(x, "x")
+        _check_rows(residual, "residual")
+        if x.shape != residual.shape:
+            raise ValueError("x and residual must have the same shape")
+        _lib.check(_lib.lib().aios_rmsnorm(x.data_ptr(), x.stride(0), residual.data_ptr(),
+                                           residual.stride(0), weight.data_ptr(), x.data_ptr(),
+                                           x.stride(0), x.shape[0], x.shape[1], eps, _stream(x)),
+                   "aios_rmsnorm")
+        return x, residual
+
+    @staticmethod
+    def qk_norm_rope(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                     cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
+                     num_qo_heads: int, num_kv_heads: int, head_dim: int,
+                     eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+        """q, k = RoPE(RMSNorm_head(q)), RoPE(RMSNorm_head(k)) from qkv rows."""
+        _check_rows(qkv, "qkv")
+        if positions.dtype != torch.int32 or positions.numel() != qkv.shape[0]:
+            raise ValueError("positions must be int32 with one entry per token")
+        if cos.dtype != torch.float32 or cos.shape != sin.shape or cos.shape[1] != head_dim:
+            raise ValueError("cos/sin tables must be float32 [positions, head_dim]")
+        t = qkv.shape[0]
+        q = torch.empty(t, num_qo_heads, head_dim, dtype=qkv.dtype, device=qkv.device)
+        k = torch.empty(t, num_kv_heads, head_dim, dtype=qkv.dtype, device=qkv.device)
+        _lib.check(_lib.lib().aios_qk_norm_rope(
+            qkv.data_ptr(), qkv.stride(0), t, num_qo_heads, num_kv_heads, head_dim,
+            q_weight.data_ptr(), k_weight.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+            positions.contiguous().data_ptr(), q.data_ptr(), k.data_ptr(), eps, _stream(qkv)),
+            "aios_qk_norm_rope")
+        return q, k
+
+    @staticmethod
+    def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+        _check_rows(x, "x")
+        inter = x.shape[1] // 2
+        out = torch.empty(x.shape[0], inter, dtype=x.dtype, device=x.device)
+        _lib.check(_lib.lib().aios_silu_mul(x.data_ptr(), x.stride(0), x.shape[0], inter,
+                                            out.data_ptr(), out.stride(0), _stream(x)),
+                   "aios_silu_mul")
+        return out

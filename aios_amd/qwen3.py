@@ -2,12 +2,13 @@
 
 Restates python/aios/models/qwen3.py:31-173 and the layer ops it uses
 (python/aios/layers/norm.py:10-40, activation.py:9-12, rotary.py:8-29,
-attention.py:6-16, embedding.py:13-41) without FlashInfer: RMSNorm and the
-fused residual-add RMSNorm compute in fp32 and store bf16, SiLU-and-mul and
-RoPE are plain torch ops.  Attention goes through the backend exactly as in
-the reference: ``backend.forward(q, k, v, kv_cache, layer_id, batch)`` once
-per layer with q/k/v as ``[tokens, heads, head_dim]`` (v a strided view into
-the fused qkv projection).
+attention.py:6-16, embedding.py:13-41) without FlashInfer: RMSNorm, the
+residual-add RMSNorm, per-head q/k RMSNorm + RoPE and SiLU-and-mul are the
+gfx950 kernels of aios_amd.layers (one launch each); the projections are
+torch GEMMs.  Attention goes through the backend exactly as in the
+reference: ``backend.forward(q, k, v, kv_cache, layer_id, batch)`` once per
+layer with q/k/v as ``[tokens, heads, head_dim]`` (v a strided view into the
+fused qkv projection).
 
 Weights are synthetic (seeded N(0, 0.02), norm weights 1, tied embedding);
 no checkpoint is loaded.
@@ -58,34 +59,8 @@ def weights_to(w: dict, device, dtype=None) -> dict:
             "layers": [{k: mv(v) for k, v in lw.items()} for lw in w["layers"]]}
 
 
-def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """fp32 RMSNorm, stored in the input dtype (norm.py:18-22)."""
-    xf = x.float()
-    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * weight.float()
-    return y.to(x.dtype)
-
-
-def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
-                      eps: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """residual <- x + residual; x <- RMSNorm(residual) (norm.py:34-40)."""
-    r = x.float() + residual.float()
-    y = r * torch.rsqrt(r.pow(2).mean(-1, keepdim=True) + eps) * weight.float()
-    return y.to(x.dtype), r.to(residual.dtype)
-
-
-def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
-    """silu(x[:, :I]) * x[:, I:] (activation.py:9-12)."""
-    gate, up = x.chunk(2, dim=-1)
-    return F.silu(gate) * up
-
-
-def rotate_half(x: torch.Tensor) -> torch.Tensor:
-    x1, x2 = x.chunk(2, dim=-1)
-    return torch.cat((-x2, x1), dim=-1)
-
-
 class RotaryEmbedding:
-    """cos/sin cache (rotary.py:8-29)."""
+    """fp32 cos/sin tables [max_positions, head_dim] (rotary.py:8-29)."""
 
     def __init__(self, head_dim: int, max_positions: int, base: float, device) -> None:
         inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
@@ -94,65 +69,63 @@ class RotaryEmbedding:
         self.cos = emb.cos().to(device)
         self.sin = emb.sin().to(device)
 
-    def __call__(self, positions: torch.Tensor):
-        idx = positions.long()
-        return self.cos[idx].unsqueeze(1), self.sin[idx].unsqueeze(1)
-
-
-def apply_rotary_pos_emb(q, k, cos, sin):
-    """attention.py:11-16 (cos/sin cast to the activation dtype)."""
-    cos = cos.to(q.dtype)
-    sin = sin.to(q.dtype)
-    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
-
 
 class Qwen3ForCausalLM:
     """Decoder + tied LM head.  ``forward()`` reads the batch from the global
-    context like the reference (qwen3.py:140-173)."""
+    context like the reference (qwen3.py:140-173).  ``ops`` supplies rmsnorm,
+    fused_add_rmsnorm, qk_norm_rope and silu_and_mul (default: the gfx950
+    kernels, aios_amd.layers.HipOps)."""
 
     def __init__(self, config: ModelConfig, weights: dict, device,
                  attn_backend: BaseAttentionBackend | None = None,
-                 max_positions: int | None = None) -> None:
+                 max_positions: int | None = None, ops=None) -> None:
         self.config = config
         self.device = torch.device(device)
         self.w = weights
         self.attn_backend = attn_backend or Mi355xAttentionBackend(config)
+        if ops is None:
+            from aios_amd.layers import HipOps
+
+            ops = HipOps()
+        self.ops = ops
         self.rotary = RotaryEmbedding(config.head_dim,
                                       max_positions or min(config.max_position_embeddings, 8192),
                                       config.rope_theta, self.device)
         self._q_size = config.num_qo_heads * config.head_dim
         self._kv_size = config.num_kv_heads * config.head_dim
 
-    def _attention(self, i: int, h: torch.Tensor, cos, sin, kv_cache, batch) -> torch.Tensor:
+    def _attention(self, i: int, h: torch.Tensor, positions, kv_cache, batch) -> torch.Tensor:
+        """qwen3.py:52-75: qkv projection, per-head q/k RMSNorm + RoPE, the
+        backend, o_proj (v stays a strided view into qkv, as in the reference)."""
         c = self.config
         lw = self.w["layers"][i]
         t = h.shape[0]
         qkv = F.linear(h, lw["qkv"])
-        q, k, v = qkv.split([self._q_size, self._kv_size, self._kv_size], dim=-1)
-        q = rmsnorm(q.reshape(t, c.num_qo_heads, c.head_dim), lw["q_norm"], c.rms_norm_eps)
-        k = rmsnorm(k.reshape(t, c.num_kv_heads, c.head_dim), lw["k_norm"], c.rms_norm_eps)
-        v = v.view(t, c.num_kv_heads, c.head_dim)
-        q, k = apply_rotary_pos_emb(q, k, cos, sin)
-        out = self.attn_backend.forward(q.contiguous(), k.contiguous(), v, kv_cache, i, batch)
+        q, k = self.ops.qk_norm_rope(qkv, lw["q_norm"], lw["k_norm"], self.rotary.cos,
+                                     self.rotary.sin, positions, c.num_qo_heads, c.num_kv_heads,
+                                     c.head_dim, c.rms_norm_eps)
+        v = qkv[:, self._q_size + self._kv_size:].view(t, c.num_kv_heads, c.head_dim)
+        out = self.attn_backend.forward(q, k, v, kv_cache, i, batch)
         return F.linear(out.reshape(t, -1), lw["o"])
 
     def forward(self) -> torch.Tensor:
         ctx = get_global_ctx()
         batch = ctx.batch
         c = self.config
+        ops = self.ops
         h = F.embedding(batch.input_ids, self.w["embed"])
-        cos, sin = self.rotary(batch.positions)
+        positions = batch.positions
         residual = None
         for i, lw in enumerate(self.w["layers"]):
             if residual is None:
                 residual = h
-                x = rmsnorm(h, lw["input_norm"], c.rms_norm_eps)
+                x = ops.rmsnorm(h, lw["input_norm"], c.rms_norm_eps)
             else:
-                x, residual = fused_add_rmsnorm(h, residual, lw["input_norm"], c.rms_norm_eps)
-            x = self._attention(i, x, cos, sin, ctx.kv_cache, batch)
-            x, residual = fused_add_rmsnorm(x, residual, lw["post_norm"], c.rms_norm_eps)
-            h = F.linear(silu_and_mul(F.linear(x, lw["gate_up"])), lw["down"])
-        x, _ = fused_add_rmsnorm(h, residual, self.w["final_norm"], c.rms_norm_eps)
+                x, residual = ops.fused_add_rmsnorm(h, residual, lw["input_norm"], c.rms_norm_eps)
+            x = self._attention(i, x, positions, ctx.kv_cache, batch)
+            x, residual = ops.fused_add_rmsnorm(x, residual, lw["post_norm"], c.rms_norm_eps)
+            h = F.linear(ops.silu_and_mul(F.linear(x, lw["gate_up"])), lw["down"])
+        x, _ = ops.fused_add_rmsnorm(h, residual, self.w["final_norm"], c.rms_norm_eps)
         if batch.is_prefill and not batch.return_all_logits:
             x = x[batch.attn_metadata.get_last_indices(batch.size)]
         return F.linear(x, self.w["embed"])

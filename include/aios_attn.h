@@ -26,6 +26,10 @@
  *   aios_build_indices the device half of prepare_metadata's
  *                      torch.cat([page_table[row, :device_len] ...])
  *                      (python/aios/attention/flashinfer.py:228-230)
+ *   aios_rmsnorm, aios_qk_norm_rope, aios_silu_mul  the decoder-layer
+ *                      elementwise ops that produce the backend's inputs
+ *                      (python/aios/layers/norm.py:18-40, models/qwen3.py:
+ *                      60-70, layers/attention.py:11-16, activation.py:9-12)
  *   aios_greedy_select the greedy branch of Sampler.sample_with_logprobs
  *                      (python/aios/engine/sample.py:73, 115-117): argmax of
  *                      the logits plus the raw log_softmax value gathered
@@ -199,6 +203,44 @@ int aios_build_indices(const int32_t* page_table, int64_t page_table_stride,
                        const int32_t* row_ids, const int32_t* cu_k,
                        int32_t batch_size, int32_t total_kv,
                        int32_t* indices_out, void* stream);
+
+/*
+ * RMSNorm over rows of bf16 hidden states (hidden a multiple of 8, <= 8192;
+ * rows 16-byte aligned), fp32 math:
+ *   residual == NULL: out = x * rsqrt(mean(x^2) + eps) * weight
+ *   otherwise:        r = x + residual; residual <- r (bf16);
+ *                     out = r * rsqrt(mean(r^2) + eps) * weight
+ * Replaces flashinfer rmsnorm / fused_add_rmsnorm behind RMSNorm and
+ * RMSNormFused (python/aios/layers/norm.py:18-40).  out may alias x.
+ */
+int aios_rmsnorm(const void* x, int64_t x_stride, void* residual, int64_t residual_stride,
+                 const void* weight, void* out, int64_t out_stride, int64_t rows, int32_t hidden,
+                 float eps, void* stream);
+
+/*
+ * Per-head query/key RMSNorm followed by rotary embedding, from the fused
+ * qkv projection rows [tokens][(Hq + 2*Hkv) * D] (row stride qkv_stride):
+ *   x' = bf16(x * rsqrt(mean(x^2) + eps) * w)                (q or k weight)
+ *   out_i = bf16(bf16(x'_i * c_i) + bf16(rot(x')_i * s_i)),  rot = rotate_half
+ * with c, s = bf16(cos/sin_table[positions[t]][i]) (fp32 tables of
+ * table_rows x D; positions outside [0, table_rows) are clamped into it).
+ * q_out is [tokens][Hq][D], k_out [tokens][Hkv][D].
+ * Replaces q_norm / k_norm (python/aios/models/qwen3.py:65-66) and
+ * apply_rotary_pos_emb (python/aios/layers/attention.py:11-16).
+ */
+int aios_qk_norm_rope(const void* qkv, int64_t qkv_stride, int64_t tokens, int32_t num_qo_heads,
+                      int32_t num_kv_heads, int32_t head_dim, const void* q_weight,
+                      const void* k_weight, const float* cos_table, const float* sin_table,
+                      int64_t table_rows, const int32_t* positions, void* q_out, void* k_out,
+                      float eps, void* stream);
+
+/*
+ * out[r][i] = bf16(bf16(silu(x[r][i])) * x[r][intermediate + i]) for the
+ * merged gate/up rows x [rows][2 * intermediate].  Replaces silu_and_mul
+ * (python/aios/layers/activation.py:9-12).
+ */
+int aios_silu_mul(const void* x, int64_t x_stride, int64_t rows, int32_t intermediate, void* out,
+                  int64_t out_stride, void* stream);
 
 /*
  * Greedy selection over rows of logits (elem_bytes 2: bf16, 4: fp32):

@@ -1,0 +1,71 @@
+"""Decoder-layer kernels (aios_rmsnorm, aios_qk_norm_rope, aios_silu_mul) vs
+the torch formulas of the reference layers on the same bf16 inputs."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from aios_amd.layers import HipOps
+from aios_amd.qwen3 import RotaryEmbedding
+from tests.util import TorchOps
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _bf16(shape, seed, scale=1.0):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return (torch.randn(shape, generator=g, device=DEV) * scale).to(torch.bfloat16)
+
+
+def _ulp_close(a, b, ulps=1):
+    """bf16 results within `ulps` units in the last place (relative 2^-7 per ulp)."""
+    a, b = a.float(), b.float()
+    tol = ulps * 2.0 ** -7 * torch.maximum(a.abs(), b.abs()) + 1e-6
+    assert bool(((a - b).abs() <= tol).all()), (a - b).abs().max().item()
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 768), (8, 768), (37, 1024), (5, 2560), (3, 8192)])
+def test_rmsnorm_and_fused_add(rows, hidden):
+    x = _bf16((rows, hidden), rows, 2.0)
+    r = _bf16((rows, hidden), rows + 1, 3.0)
+    w = _bf16((hidden,), 7).abs() + 0.5
+    ops, ref = HipOps(), TorchOps()
+    _ulp_close(ops.rmsnorm(x, w, 1e-5), ref.rmsnorm(x, w, 1e-5))
+    x1, r1 = x.clone(), r.clone()
+    x2, r2 = x.clone(), r.clone()
+    ops.fused_add_rmsnorm(x1, r1, w, 1e-6)
+    ref.fused_add_rmsnorm(x2, r2, w, 1e-6)
+    assert torch.equal(r1, r2)  # the residual sum is rounded once, as in the reference
+    _ulp_close(x1, x2)
+
+
+def test_rmsnorm_rejects_unsupported_width():
+    with pytest.raises(ValueError, match="multiple of 8"):
+        HipOps().rmsnorm(_bf16((2, 100), 1), _bf16((100,), 2), 1e-6)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 96), (12, 4, 64), (16, 8, 128), (32, 8, 128)])
+def test_qk_norm_rope(hq, hkv, d):
+    t = 19
+    qkv = _bf16((t, (hq + 2 * hkv) * d), d + hq, 1.5)
+    qw = _bf16((d,), 3).abs() + 0.5
+    kw = _bf16((d,), 4).abs() + 0.5
+    rot = RotaryEmbedding(d, 512, 1000000.0, DEV)
+    pos = torch.tensor([0, 1, 2, 5, 31, 32, 100, 511] + list(range(200, 211)), dtype=torch.int32,
+                       device=DEV)
+    q1, k1 = HipOps().qk_norm_rope(qkv, qw, kw, rot.cos, rot.sin, pos, hq, hkv, d, 1e-6)
+    q2, k2 = TorchOps().qk_norm_rope(qkv, qw, kw, rot.cos, rot.sin, pos, hq, hkv, d, 1e-6)
+    # Same roundings as the torch ops; the norm's fp32 sum may differ in the
+    # last bit, which can move an output by one bf16 step.
+    _ulp_close(q1, q2, ulps=2)
+    _ulp_close(k1, k2, ulps=2)
+    # position 0 is the identity rotation: the output is the normalised head
+    xn = TorchOps()._norm(qkv[:1, : hq * d].reshape(1, hq, d), qw, 1e-6)
+    _ulp_close(q1[:1], xn)
+
+
+@pytest.mark.parametrize("rows,inter", [(8, 2048), (32, 3072), (3, 9728)])
+def test_silu_and_mul(rows, inter):
+    x = _bf16((rows, 2 * inter), inter, 2.0)
+    _ulp_close(HipOps().silu_and_mul(x), TorchOps().silu_and_mul(x))

@@ -372,7 +372,9 @@ def test_oracle_model_matches_product_decoder_composition():
             lw[key].uniform_(0.5, 1.5)
     ids = torch.tensor([5, 9, 2, 44, 0, 13])
     backend = _DenseCpuBackend(c.head_dim ** -0.5)
-    model = Qwen3ForCausalLM(c, w, "cpu", attn_backend=backend, max_positions=64)
+    from tests.util import TorchOps
+
+    model = Qwen3ForCausalLM(c, w, "cpu", attn_backend=backend, max_positions=64, ops=TorchOps())
     reset_global_ctx()
     ctx = Context(page_size=1)
     ctx.kv_cache = None

@@ -19,3 +19,42 @@ def bits(t: torch.Tensor) -> np.ndarray:
 def assert_close_bf16(actual: torch.Tensor, expected: np.ndarray, atol=1e-2, rtol=1e-2):
     a = to_np64(actual)
     np.testing.assert_allclose(a, expected, atol=atol, rtol=rtol)
+
+
+class TorchOps:
+    """The decoder op set (aios_amd.layers.HipOps interface) as plain torch
+    math: the reference formulas of layers/norm.py:18-40 (fp32),
+    models/qwen3.py:65-66 + layers/attention.py:11-16 (bf16 RoPE products
+    when the input is bf16) and layers/activation.py:9-12.  Test helper."""
+
+    @staticmethod
+    def _norm(x, weight, eps):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * weight.float()).to(x.dtype)
+
+    def rmsnorm(self, x, weight, eps):
+        return self._norm(x, weight, eps)
+
+    def fused_add_rmsnorm(self, x, residual, weight, eps):
+        r = x.float() + residual.float()
+        y = r * torch.rsqrt(r.pow(2).mean(-1, keepdim=True) + eps) * weight.float()
+        residual.copy_(r.to(residual.dtype))
+        x.copy_(y.to(x.dtype))
+        return x, residual
+
+    def qk_norm_rope(self, qkv, q_weight, k_weight, cos, sin, positions, hq, hkv, d, eps):
+        t = qkv.shape[0]
+        q = self._norm(qkv[:, : hq * d].reshape(t, hq, d), q_weight, eps)
+        k = self._norm(qkv[:, hq * d : (hq + hkv) * d].reshape(t, hkv, d), k_weight, eps)
+        c = cos[positions.long()].unsqueeze(1).to(q.dtype)
+        s = sin[positions.long()].unsqueeze(1).to(q.dtype)
+
+        def rot(x):
+            x1, x2 = x.chunk(2, dim=-1)
+            return torch.cat((-x2, x1), dim=-1)
+
+        return q * c + rot(q) * s, k * c + rot(k) * s
+
+    def silu_and_mul(self, x):
+        g, u = x.chunk(2, dim=-1)
+        return torch.nn.functional.silu(g) * u
