@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "aios_rmsnorm",
     "aios_qk_norm_rope",
     "aios_silu_mul",
+    "aios_linear_rows",
     "aios_greedy_select",
 )
 
@@ -119,6 +120,8 @@ def _declare(lib: ctypes.CDLL) -> None:
                                       _vp, _vp, _vp, _f32, _vp]
     lib.aios_silu_mul.restype = ctypes.c_int
     lib.aios_silu_mul.argtypes = [_vp, _i64, _i64, _i32, _vp, _i64, _vp]
+    lib.aios_linear_rows.restype = ctypes.c_int
+    lib.aios_linear_rows.argtypes = [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp]
     lib.aios_greedy_select.restype = ctypes.c_int
     lib.aios_greedy_select.argtypes = [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]
 

@@ -438,6 +438,25 @@ int aios_silu_mul(const void* x, int64_t x_stride, int64_t rows, int32_t interme
                    "silu_mul launch");
 }
 
+int aios_linear_rows(const void* x, int64_t x_stride, const void* weight, int64_t w_stride,
+                     void* y, int64_t y_stride, int64_t rows, int64_t out_features,
+                     int64_t in_features, void* stream) {
+  if (!aios::skinny_gemm_supported(rows, out_features, in_features))
+    return fail(AIOS_ERR_UNSUPPORTED,
+                "linear_rows: needs 1..64 rows, out_features %% 16 == 0, in_features %% 128 == 0 "
+                "(got %lld x %lld x %lld)",
+                (long long)rows, (long long)out_features, (long long)in_features);
+  if (!x || !weight || !y) return fail(AIOS_ERR_INVALID, "linear_rows: null pointer");
+  if (x_stride < in_features || w_stride < in_features || y_stride < out_features ||
+      (x_stride | w_stride) % 8 != 0 || y_stride % 4 != 0)
+    return fail(AIOS_ERR_INVALID, "linear_rows: bad row strides");
+  if ((((uintptr_t)x | (uintptr_t)weight) & 15) != 0 || ((uintptr_t)y & 7) != 0)
+    return fail(AIOS_ERR_INVALID, "linear_rows: misaligned rows");
+  return check_hip(aios::skinny_gemm(x, x_stride, weight, w_stride, y, y_stride, rows, out_features,
+                                     in_features, static_cast<hipStream_t>(stream)),
+                   "linear_rows launch");
+}
+
 int aios_greedy_select(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
                        int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                        void* stream) {

@@ -107,6 +107,10 @@ hipError_t qk_norm_rope(const void* qkv, int64_t stride, int64_t tokens, int hq,
 hipError_t silu_mul(const void* x, int64_t x_stride, int64_t rows, int inter, void* out,
                     int64_t out_stride, hipStream_t stream);
 
+bool skinny_gemm_supported(int64_t M, int64_t N, int64_t K);
+hipError_t skinny_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_stride, void* y,
+                       int64_t y_stride, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
 hipError_t greedy_select(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
                          int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                          hipStream_t stream);

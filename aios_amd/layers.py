@@ -23,7 +23,25 @@ def _check_rows(t: torch.Tensor, name: str) -> None:
 
 
 class HipOps:
-    """RMSNorm, residual-add RMSNorm, q/k RMSNorm + RoPE, SiLU-and-mul."""
+    """RMSNorm, residual-add RMSNorm, q/k RMSNorm + RoPE, SiLU-and-mul, and
+    the projections (few-row GEMM kernel for decode-sized inputs, the
+    library GEMM for larger ones)."""
+
+    @staticmethod
+    def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        rows, k = x.shape
+        n = weight.shape[0]
+        if (rows > 64 or n % 16 or k % 128 or x.dtype != torch.bfloat16
+                or weight.dtype != torch.bfloat16 or x.stride(1) != 1 or weight.stride(1) != 1
+                or x.stride(0) % 8 or weight.stride(0) % 8):
+            return torch.nn.functional.linear(x, weight)
+        if rows == 0:
+            return x.new_empty(0, n)
+        y = torch.empty(rows, n, dtype=x.dtype, device=x.device)
+        _lib.check(_lib.lib().aios_linear_rows(x.data_ptr(), x.stride(0), weight.data_ptr(),
+                                               weight.stride(0), y.data_ptr(), y.stride(0), rows,
+                                               n, k, _stream(x)), "aios_linear_rows")
+        return y
 
     @staticmethod
     def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:

@@ -72,9 +72,9 @@ class RotaryEmbedding:
 
 class Qwen3ForCausalLM:
     """Decoder + tied LM head.  ``forward()`` reads the batch from the global
-    context like the reference (qwen3.py:140-173).  ``ops`` supplies rmsnorm,
-    fused_add_rmsnorm, qk_norm_rope and silu_and_mul (default: the gfx950
-    kernels, aios_amd.layers.HipOps)."""
+    context like the reference (qwen3.py:140-173).  ``ops`` supplies linear,
+    rmsnorm, fused_add_rmsnorm, qk_norm_rope and silu_and_mul (default: the
+    gfx950 kernels, aios_amd.layers.HipOps)."""
 
     def __init__(self, config: ModelConfig, weights: dict, device,
                  attn_backend: BaseAttentionBackend | None = None,
@@ -100,13 +100,13 @@ class Qwen3ForCausalLM:
         c = self.config
         lw = self.w["layers"][i]
         t = h.shape[0]
-        qkv = F.linear(h, lw["qkv"])
+        qkv = self.ops.linear(h, lw["qkv"])
         q, k = self.ops.qk_norm_rope(qkv, lw["q_norm"], lw["k_norm"], self.rotary.cos,
                                      self.rotary.sin, positions, c.num_qo_heads, c.num_kv_heads,
                                      c.head_dim, c.rms_norm_eps)
         v = qkv[:, self._q_size + self._kv_size:].view(t, c.num_kv_heads, c.head_dim)
         out = self.attn_backend.forward(q, k, v, kv_cache, i, batch)
-        return F.linear(out.reshape(t, -1), lw["o"])
+        return self.ops.linear(out.reshape(t, -1), lw["o"])
 
     def forward(self) -> torch.Tensor:
         ctx = get_global_ctx()
@@ -124,8 +124,8 @@ class Qwen3ForCausalLM:
                 x, residual = ops.fused_add_rmsnorm(h, residual, lw["input_norm"], c.rms_norm_eps)
             x = self._attention(i, x, positions, ctx.kv_cache, batch)
             x, residual = ops.fused_add_rmsnorm(x, residual, lw["post_norm"], c.rms_norm_eps)
-            h = F.linear(ops.silu_and_mul(F.linear(x, lw["gate_up"])), lw["down"])
+            h = ops.linear(ops.silu_and_mul(ops.linear(x, lw["gate_up"])), lw["down"])
         x, _ = ops.fused_add_rmsnorm(h, residual, self.w["final_norm"], c.rms_norm_eps)
         if batch.is_prefill and not batch.return_all_logits:
             x = x[batch.attn_metadata.get_last_indices(batch.size)]
-        return F.linear(x, self.w["embed"])
+        return ops.linear(x, self.w["embed"])

@@ -30,6 +30,8 @@
  *                      elementwise ops that produce the backend's inputs
  *                      (python/aios/layers/norm.py:18-40, models/qwen3.py:
  *                      60-70, layers/attention.py:11-16, activation.py:9-12)
+ *   aios_linear_rows   F.linear of the few-row decode projections
+ *                      (python/aios/layers/linear.py:11-60)
  *   aios_greedy_select the greedy branch of Sampler.sample_with_logprobs
  *                      (python/aios/engine/sample.py:73, 115-117): argmax of
  *                      the logits plus the raw log_softmax value gathered
@@ -241,6 +243,19 @@ int aios_qk_norm_rope(const void* qkv, int64_t qkv_stride, int64_t tokens, int32
  */
 int aios_silu_mul(const void* x, int64_t x_stride, int64_t rows, int32_t intermediate, void* out,
                   int64_t out_stride, void* stream);
+
+/*
+ * y[r][n] = sum_k x[r][k] * weight[n][k] (bf16 in, fp32 accumulate, bf16
+ * out) for 1..64 rows, out_features a multiple of 16 and in_features a
+ * multiple of 128: the projections of a decode step (F.linear behind
+ * Linear / LinearQKVMerged / LinearColParallelMerged,
+ * python/aios/layers/linear.py:11-60, and the tied LM head,
+ * python/aios/layers/embedding.py:13-41).  Returns AIOS_ERR_UNSUPPORTED for
+ * other shapes (callers use a library GEMM there).
+ */
+int aios_linear_rows(const void* x, int64_t x_stride, const void* weight, int64_t w_stride,
+                     void* y, int64_t y_stride, int64_t rows, int64_t out_features,
+                     int64_t in_features, void* stream);
 
 /*
  * Greedy selection over rows of logits (elem_bytes 2: bf16, 4: fp32):

@@ -69,3 +69,28 @@ def test_qk_norm_rope(hq, hkv, d):
 def test_silu_and_mul(rows, inter):
     x = _bf16((rows, 2 * inter), inter, 2.0)
     _ulp_close(HipOps().silu_and_mul(x), TorchOps().silu_and_mul(x))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1152, 768), (8, 1152, 768), (8, 768, 768), (8, 4096, 768),
+                                   (8, 768, 2048), (8, 6400, 768), (24, 1024, 4096),
+                                   (17, 2048, 1024), (64, 256, 9728), (33, 16, 128)])
+def test_linear_rows_matches_fp32_gemm(m, n, k):
+    """Few-row GEMM kernel vs an fp32 matmul of the same bf16 operands: fp32
+    accumulation, one bf16 rounding at the end."""
+    x = _bf16((m, k), m + k, 1.0)
+    w = _bf16((n, k), n, 0.05)
+    y = HipOps().linear(x, w)
+    ref = (x.float() @ w.float().T)
+    err = (y.float() - ref).abs()
+    assert bool((err <= 2.0 ** -8 * ref.abs() + 1e-3 * ref.abs().max()).all()), err.max().item()
+
+
+def test_linear_rows_strided_input_and_fallback():
+    x_big = _bf16((8, 2048), 5)
+    x = x_big[:, :768]  # row stride 2048
+    w = _bf16((1152, 768), 6, 0.05)
+    torch.testing.assert_close(HipOps().linear(x, w).float(), (x.float() @ w.float().T),
+                               atol=2e-2, rtol=1e-2)
+    x65 = _bf16((65, 768), 7)  # more rows than the kernel takes: library GEMM
+    torch.testing.assert_close(HipOps().linear(x65, w).float(), (x65.float() @ w.float().T),
+                               atol=2e-2, rtol=1e-2)

@@ -58,3 +58,6 @@ class TorchOps:
     def silu_and_mul(self, x):
         g, u = x.chunk(2, dim=-1)
         return torch.nn.functional.silu(g) * u
+
+    def linear(self, x, weight):
+        return torch.nn.functional.linear(x, weight)
