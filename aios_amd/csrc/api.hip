@@ -155,8 +155,8 @@ int aios_attn_plan(int32_t phase, const int32_t* cu_q, const int32_t* cu_k, int3
     n_chunks = cdiv(P, chunk);
   }
   const int32_t max_suffix = max_kv - P;
-  const int32_t pass = aios::kSuffixPass;  // KV positions one suffix wavefront loads at once
-  const int32_t tpg = pass / 4;
+  const int32_t pass = aios::kSuffixPass;  // KV positions one suffix workgroup loads at once
+  const int32_t tpg = pass / 4;             // per wavefront
   int32_t split;
   if (suffix_split_len > 0) {
     split = suffix_split_len;

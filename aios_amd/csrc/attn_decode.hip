@@ -92,20 +92,27 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
 }
 
 // ---------------------------------------------------------------------------
-// suffix part: one wavefront per (row, kv-head, split) item.  The wavefront
-// gathers 32 positions at a time of the row's own pages into its own LDS
-// sub-tile (the engine's layout) and runs the engine math with one 16-row
-// MFMA tile whose first G rows are the row's query heads.
+// suffix part: one workgroup per (row, kv-head, split) item.  Its four
+// wavefronts take the item's 32-position sub-tiles round-robin; each gathers
+// its sub-tile of the row's own pages into its own LDS region (the engine's
+// layout) and runs the engine math with one 16-row MFMA tile whose first G
+// rows are the row's query heads.  The four softmax states are then merged
+// through LDS by the first wavefront.
 template <int D, int G>
-__device__ __forceinline__ void decode_suffix_item(uint8_t* buf, const DecodeArgs& a, int item) {
+__device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArgs& a, int item) {
   using T = KVTile<D>;
   constexpr int CH = T::SUB_BYTES / 16;  // 16-byte chunks per sub-tile (K then V)
   constexpr int NJ = CH / 64;            // DMA loads per lane per sub-tile
+  constexpr int NW = kEngineThreads / 64;
+  constexpr int DT = D / 16;
   static_assert(CH % 64 == 0, "sub-tile must split over one wavefront");
   static_assert(G <= 16, "one MFMA row tile");
+  static_assert(DT * 64 * 16 + 2 * 16 * 4 <= T::SUB_BYTES, "merge state fits the wave region");
   const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int l16 = lane & 15;
   const int lg = lane >> 4;
+  uint8_t* buf = lds + wave * T::SUB_BYTES;
   const int split = item % a.n_splits;
   const int bh = item / a.n_splits;
   const int h = bh % a.num_kv_heads;
@@ -123,12 +130,12 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* buf, const DecodeArg
 
   // Fused append: the row's last position is its new token, gathered from
   // k_new / v_new (page selector kNewTok) and written to its page below (no
-  // other workgroup of the launch reads that page).
+  // other workgroup of the launch reads that page).  A slot outside the pool
+  // is not written, and the row then attends to zeros there, as the separate
+  // append and decode would.
   constexpr uint32_t kNoPage = 0xffffffffu;
   constexpr uint32_t kNewTok = 0xfffffffeu;
   const int t_new = a.k_new != nullptr ? kv_len - 1 : -1;
-  // A slot outside the pool is not written, and the row then attends to
-  // zeros there, as the separate append and decode would.
   const int64_t new_dst = a.k_new != nullptr ? (int64_t)a.out_loc[b] : -1;
   const bool new_ok = (uint64_t)new_dst < (uint64_t)a.num_pages;
   const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2;
@@ -157,7 +164,7 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* buf, const DecodeArg
     isv_j[j] = isv;
     coff_j[j] = (uint32_t)((isv ? T::v_chunk(t, slot) : T::k_chunk(t, slot)) * 16);
   }
-  for (int kv0 = s_begin; kv0 < s_end; kv0 += kSubTok) {
+  for (int kv0 = s_begin + wave * kSubTok; kv0 < s_end; kv0 += NW * kSubTok) {
     const int pos = kv0 + lane;
     uint32_t sel = kNoPage;
     if (lane < kSubTok && pos < s_end)
@@ -176,21 +183,62 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* buf, const DecodeArg
   }
   eng.finish();
 
-  if (new_ok && t_new >= s_begin && t_new < s_end && lane < 2 * T::CPR) {
+  if (new_ok && t_new >= s_begin && t_new < s_end &&
+      ((t_new - s_begin) / kSubTok) % NW == wave && lane < 2 * T::CPR) {
     const bool isv = lane >= T::CPR;
     const int c = isv ? lane - T::CPR : lane;
     const uint4 v = *reinterpret_cast<const uint4*>((isv ? vn : kn) + c * 16);
     *reinterpret_cast<uint4*>(const_cast<uint8_t*>(isv ? vc : kc) + new_dst * tok_b + c * 16) = v;
   }
 
+  // Merge the four wavefronts' states (o relative to each wave's reference
+  // m, row totals l) through LDS.
+  f32x4* so = reinterpret_cast<f32x4*>(buf);
+  float* sm = reinterpret_cast<float*>(buf + DT * 64 * 16);
+  float* sl = sm + 16;
+  if (wave > 0) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) so[dt * 64 + lane] = eng.o[0][dt];
+    if (lg == 0) {
+      sm[l16] = eng.m_run[0];
+      sl[l16] = eng.l_run[0];
+    }
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  float mw[NW], lw[NW];
+  mw[0] = eng.m_run[0];
+  lw[0] = eng.l_run[0];
+  float mx = mw[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    const float* smw = reinterpret_cast<const float*>(lds + w * T::SUB_BYTES + DT * 64 * 16);
+    mw[w] = smw[l16];
+    lw[w] = smw[16 + l16];
+    mx = fmaxf(mx, mw[w]);
+  }
+  float f[NW];
+  float l_tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    f[w] = (mw[w] == kNegInf) ? 0.f : fast_exp2(mw[w] - mx);
+    l_tot += lw[w] * f[w];
+  }
+  f32x4 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    acc[dt] = eng.o[0][dt] * f[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w)
+      acc[dt] += reinterpret_cast<const f32x4*>(lds + w * T::SUB_BYTES)[dt * 64 + lane] * f[w];
+  }
+
   if (l16 >= G) return;
-  constexpr int DT = D / 16;
-  const float l_tot = eng.l_run[0];
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   const int row = b * G + l16;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
-    const f32x4 v = eng.o[0][dt] * inv;
+    const f32x4 v = acc[dt] * inv;
     uint2 packed;
     packed.x = pack_bf16x2(v[0], v[1]);
     packed.y = pack_bf16x2(v[2], v[3]);
@@ -202,7 +250,7 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* buf, const DecodeArg
   }
   if (!a.final_out && lg == 0)
     a.parts.lse[a.parts.lse_index(h, a.parts.n_chunks + split, row)] =
-        l_tot > 0.f ? eng.m_run[0] + fast_log2(l_tot) : kNegInf;
+        l_tot > 0.f ? mx + fast_log2(l_tot) : kNegInf;
 }
 
 template <int D, int G>
@@ -212,10 +260,7 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
   if (wg < a.prefix_wgs) {
     decode_prefix_part<D>(lds, a, wg);
   } else {
-    const int wave = threadIdx.x >> 6;
-    const int item = (wg - a.prefix_wgs) * (kEngineThreads / 64) + wave;
-    if (item < a.suffix_items)
-      decode_suffix_item<D, G>(lds + wave * KVTile<D>::SUB_BYTES, a, item);
+    decode_suffix_item<D, G>(lds, a, wg - a.prefix_wgs);
   }
 }
 
@@ -223,7 +268,7 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
 // combine: one workgroup per (row, kv-head)
 constexpr int kCombineThreads = 256;
 constexpr int kCombineMaxParts = 64;
-constexpr int kCombineBatch = 16;  // parts whose o loads one thread keeps in flight
+constexpr int kCombineBatch = 32;  // parts whose o loads one thread keeps in flight
 
 template <int D, int G>
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeArgs a) {
@@ -323,7 +368,7 @@ bool group_supported(int G) {
 
 template <int D, int G>
 static hipError_t launch_main_dg(const DecodeArgs& a, hipStream_t s) {
-  const int suffix_wgs = (a.suffix_items + kEngineThreads / 64 - 1) / (kEngineThreads / 64);
+  const int suffix_wgs = a.suffix_items;
   const dim3 grid(a.prefix_wgs + suffix_wgs);
   if (grid.x == 0) return hipSuccess;
   hipLaunchKernelGGL((decode_main_kernel<D, G>), grid, dim3(kEngineThreads), 0, s, a);

@@ -115,11 +115,12 @@ hipError_t greedy_select(const void* logits, int64_t row_stride, int32_t rows, i
                          int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                          hipStream_t stream);
 
-// KV positions a suffix wavefront gathers per pass (one engine sub-tile).
-constexpr int kSuffixPass = 32;
+// KV positions a suffix workgroup gathers per pass (one 32-position engine
+// sub-tile per wavefront).
+constexpr int kSuffixPass = 128;
 
 // One launch: prefix-chunk workgroups (MFMA tile engine) followed by suffix
-// workgroups (four (row, head, split) items per workgroup, one per wavefront).
+// workgroups (one (row, head, split) item per workgroup).
 hipError_t launch_decode_main(int D, const DecodeArgs& a, hipStream_t stream);
 
 // Log-sum-exp merge of every part of each (row, kv-head) into bf16 out.

@@ -103,7 +103,7 @@ typedef struct aios_attn_plan {
   int32_t cascade_mgroups;   /* 128-row groups of cascade_rows */
   int32_t suffix_split_len;  /* KV positions per suffix item */
   int32_t num_suffix_splits; /* suffix items per (row, kv-head) */
-  int32_t suffix_tpg;        /* KV positions a suffix wavefront gathers per pass, / 4 */
+  int32_t suffix_tpg;        /* KV positions a suffix wavefront gathers per pass */
   int32_t num_parts;         /* partial states per (row, kv-head); 1 = direct output */
   /* prefill */
   int32_t prefill_q_tile;    /* query tokens per workgroup */
