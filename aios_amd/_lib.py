@@ -19,6 +19,10 @@ AIOS_ERR_LAUNCH = 4
 
 PHASE_PREFILL = 0
 PHASE_DECODE = 1
+PROLOGUE_NONE = 0
+PROLOGUE_ADD_RMSNORM = 1
+EPILOGUE_NONE = 0
+EPILOGUE_SILU_MUL = 1
 
 # Every symbol include/aios_attn.h declares.
 EXPORTED_SYMBOLS = (
@@ -34,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "aios_qk_norm_rope",
     "aios_silu_mul",
     "aios_linear_rows",
+    "aios_linear_rows_ex",
     "aios_greedy_select",
 )
 
@@ -122,6 +127,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.aios_silu_mul.argtypes = [_vp, _i64, _i64, _i32, _vp, _i64, _vp]
     lib.aios_linear_rows.restype = ctypes.c_int
     lib.aios_linear_rows.argtypes = [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp]
+    lib.aios_linear_rows_ex.restype = ctypes.c_int
+    lib.aios_linear_rows_ex.argtypes = [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i32,
+                                        _vp, _i64, _vp, _f32, _vp, _i64, _i32, _vp]
     lib.aios_greedy_select.restype = ctypes.c_int
     lib.aios_greedy_select.argtypes = [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]
 

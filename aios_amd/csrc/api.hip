@@ -441,19 +441,64 @@ int aios_silu_mul(const void* x, int64_t x_stride, int64_t rows, int32_t interme
 int aios_linear_rows(const void* x, int64_t x_stride, const void* weight, int64_t w_stride,
                      void* y, int64_t y_stride, int64_t rows, int64_t out_features,
                      int64_t in_features, void* stream) {
+  return aios_linear_rows_ex(x, x_stride, weight, w_stride, y, y_stride, rows, out_features,
+                             in_features, AIOS_PROLOGUE_NONE, nullptr, 0, nullptr, 0.f, nullptr,
+                             0, AIOS_EPILOGUE_NONE, stream);
+}
+
+int aios_linear_rows_ex(const void* x, int64_t x_stride, const void* weight, int64_t w_stride,
+                        void* y, int64_t y_stride, int64_t rows, int64_t out_features,
+                        int64_t in_features, int32_t prologue, const void* residual,
+                        int64_t residual_stride, const void* norm_weight, float eps,
+                        void* residual_out, int64_t residual_out_stride, int32_t epilogue,
+                        void* stream) {
   if (!aios::skinny_gemm_supported(rows, out_features, in_features))
     return fail(AIOS_ERR_UNSUPPORTED,
                 "linear_rows: needs 1..64 rows, out_features %% 16 == 0, in_features %% 128 == 0 "
                 "(got %lld x %lld x %lld)",
                 (long long)rows, (long long)out_features, (long long)in_features);
+  if (prologue != AIOS_PROLOGUE_NONE && prologue != AIOS_PROLOGUE_ADD_RMSNORM)
+    return fail(AIOS_ERR_INVALID, "linear_rows: unknown prologue %d", prologue);
+  if (epilogue != AIOS_EPILOGUE_NONE && epilogue != AIOS_EPILOGUE_SILU_MUL)
+    return fail(AIOS_ERR_INVALID, "linear_rows: unknown epilogue %d", epilogue);
+  if (prologue == AIOS_PROLOGUE_ADD_RMSNORM && !aios::skinny_gemm_norm_supported(rows, in_features))
+    return fail(AIOS_ERR_UNSUPPORTED, "linear_rows: RMSNorm prologue for %lld rows x %lld",
+                (long long)rows, (long long)in_features);
   if (!x || !weight || !y) return fail(AIOS_ERR_INVALID, "linear_rows: null pointer");
   if (x_stride < in_features || w_stride < in_features || y_stride < out_features ||
       (x_stride | w_stride) % 8 != 0 || y_stride % 4 != 0)
     return fail(AIOS_ERR_INVALID, "linear_rows: bad row strides");
   if ((((uintptr_t)x | (uintptr_t)weight) & 15) != 0 || ((uintptr_t)y & 7) != 0)
     return fail(AIOS_ERR_INVALID, "linear_rows: misaligned rows");
-  return check_hip(aios::skinny_gemm(x, x_stride, weight, w_stride, y, y_stride, rows, out_features,
-                                     in_features, static_cast<hipStream_t>(stream)),
+  if (prologue == AIOS_PROLOGUE_ADD_RMSNORM) {
+    if (!norm_weight || ((uintptr_t)norm_weight & 15) != 0)
+      return fail(AIOS_ERR_INVALID, "linear_rows: norm weight missing or misaligned");
+    if (residual && (residual_stride < in_features || residual_stride % 8 != 0 ||
+                     ((uintptr_t)residual & 15) != 0))
+      return fail(AIOS_ERR_INVALID, "linear_rows: bad residual rows");
+    if (residual_out && (residual_out_stride < in_features || residual_out_stride % 8 != 0 ||
+                         ((uintptr_t)residual_out & 15) != 0))
+      return fail(AIOS_ERR_INVALID, "linear_rows: bad residual_out rows");
+    if (residual_out && (residual_out == x || residual_out == residual))
+      return fail(AIOS_ERR_INVALID, "linear_rows: residual_out must not alias the inputs");
+  }
+  aios::LinearArgs a = {};
+  a.x = static_cast<const aios::bf16*>(x);
+  a.x_stride = x_stride;
+  a.w = static_cast<const aios::bf16*>(weight);
+  a.w_stride = w_stride;
+  a.y = static_cast<aios::bf16*>(y);
+  a.y_stride = y_stride;
+  a.M = (int32_t)rows;
+  a.K = (int32_t)in_features;
+  a.N = out_features;
+  a.residual = static_cast<const aios::bf16*>(residual);
+  a.r_stride = residual_stride;
+  a.norm_w = static_cast<const aios::bf16*>(norm_weight);
+  a.eps = eps;
+  a.residual_out = static_cast<aios::bf16*>(residual_out);
+  a.ro_stride = residual_out_stride;
+  return check_hip(aios::skinny_gemm(a, prologue, epilogue, static_cast<hipStream_t>(stream)),
                    "linear_rows launch");
 }
 

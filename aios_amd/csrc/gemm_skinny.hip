@@ -9,78 +9,245 @@
 // y^T = W x^T with v_mfma_f32_16x16x32_bf16 (A = W rows, B = x rows), so
 // both operands are plain 16-byte row loads.  The K quarters are summed
 // through LDS and the first wavefront writes the tile.
+//
+// The ops around a projection can be folded into it, so they need no
+// launch of their own:
+//   prologue kAddNorm: x = bf16(RMSNorm(h + residual) * w) (the residual-add
+//     RMSNorm of layers/norm.py:34-40; residual may be absent), every
+//     workgroup recomputing the row norms of its few rows, and workgroup 0
+//     writing bf16(h + residual) to residual_out;
+//   epilogue kSiluPair: W holds gate rows then up rows (the merged gate/up
+//     projection); a workgroup computes gate columns n0..n0+15 and the
+//     matching up columns and writes bf16(bf16(silu(g)) * u), the
+//     silu_and_mul of layers/activation.py:9-12, with g and u rounded to
+//     bf16 first as the separate projection would store them.
 #include "kernels.hpp"
 
 namespace aios {
 namespace {
 
 constexpr int kGemmThreads = 256;
-constexpr int kGemmBatch = 8;  // k-steps whose loads are issued together
+constexpr int kGemmBatch = 8;     // k-steps whose loads are issued together
+constexpr int kNormMaxFrags = 8;  // kAddNorm holds steps * MT <= this many x fragments
 
-template <int MT>
-__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(
-    const bf16* __restrict__ x, int64_t x_stride, const bf16* __restrict__ w, int64_t w_stride,
-    bf16* __restrict__ y, int64_t y_stride, int M, int K) {
-  __shared__ f32x4 red[3][MT][64];
+enum Prologue { kPlain = 0, kAddNorm = 1 };
+enum Epilogue { kStore = 0, kSiluPair = 1 };
+
+__device__ __forceinline__ void unpack8(const bf16x8& v, float* f) {
+  const uint4 u = __builtin_bit_cast(uint4, v);
+  f[0] = lo_bf16(u.x); f[1] = hi_bf16(u.x);
+  f[2] = lo_bf16(u.y); f[3] = hi_bf16(u.y);
+  f[4] = lo_bf16(u.z); f[5] = hi_bf16(u.z);
+  f[6] = lo_bf16(u.w); f[7] = hi_bf16(u.w);
+}
+
+__device__ __forceinline__ bf16x8 pack8(const float* f) {
+  return __builtin_bit_cast(
+      bf16x8, make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]),
+                         pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])));
+}
+
+__device__ __forceinline__ float round_bf16(float x) {
+  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, static_cast<bf16>(x)) << 16);
+}
+
+template <int MT, int PRO, int EPI>
+__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a) {
+  constexpr int NP = EPI == kSiluPair ? 2 : 1;  // W row sets per workgroup
+  __shared__ f32x4 red[3][NP][MT][64];
+  __shared__ float ssq[4][MT][16];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int l16 = lane & 15;
   const int lg = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const int kq = K >> 2;  // multiple of 32
-  const int k_begin = wave * kq;
+  const int kq = a.K >> 2;  // multiple of 32
+  const int k_begin = wave * kq + lg * 8;
   const int steps = kq >> 5;
-  const bf16* wrow = w + (n0 + l16) * w_stride + k_begin + lg * 8;
-  const bf16* xrow[MT];
+  const bf16* wrow[NP];
+  wrow[0] = a.w + (n0 + l16) * a.w_stride + k_begin;
+  if constexpr (NP == 2) wrow[NP - 1] = a.w + (a.N + n0 + l16) * a.w_stride + k_begin;
+  int64_t xoff[MT], roff[MT];
   bool xok[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + l16;
-    xok[mt] = m < M;
-    xrow[mt] = x + (int64_t)(xok[mt] ? m : 0) * x_stride + k_begin + lg * 8;
+    xok[mt] = m < a.M;
+    xoff[mt] = (int64_t)(xok[mt] ? m : 0) * a.x_stride + k_begin;
+    roff[mt] = (int64_t)(xok[mt] ? m : 0) * a.r_stride + k_begin;
   }
-  f32x4 acc[MT];
+  f32x4 acc[NP][MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[p][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int s0 = 0; s0 < steps; s0 += kGemmBatch) {
-    bf16x8 a[kGemmBatch];
-    bf16x8 b[kGemmBatch][MT];
+  if constexpr (PRO == kAddNorm) {
+    // The wave's whole K quarter of its rows, r = h (+ residual) in fp32
+    // terms (kept as the bf16 operands; their fp32 sum is exact).
+    constexpr int SMAX = kNormMaxFrags / MT;
+    bf16x8 hf[SMAX][MT], rf[SMAX][MT];
+    bf16x8 wa[NP][kGemmBatch];
 #pragma unroll
-    for (int u = 0; u < kGemmBatch; ++u) {
-      if (s0 + u < steps) {
-        a[u] = *reinterpret_cast<const bf16x8*>(wrow + (s0 + u) * 32);
+    for (int p = 0; p < NP; ++p)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          b[u][mt] = xok[mt] ? *reinterpret_cast<const bf16x8*>(xrow[mt] + (s0 + u) * 32)
-                             : bf16x8{};
+      for (int u = 0; u < kGemmBatch; ++u)
+        if (u < steps) wa[p][u] = *reinterpret_cast<const bf16x8*>(wrow[p] + u * 32);
+    float ss[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) ss[mt] = 0.f;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      if (s < steps) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          hf[s][mt] = xok[mt] ? *reinterpret_cast<const bf16x8*>(a.x + xoff[mt] + s * 32)
+                              : bf16x8{};
+          rf[s][mt] = (xok[mt] && a.residual)
+                          ? *reinterpret_cast<const bf16x8*>(a.residual + roff[mt] + s * 32)
+                          : bf16x8{};
+        }
       }
     }
 #pragma unroll
-    for (int u = 0; u < kGemmBatch; ++u) {
-      if (s0 + u < steps) {
+    for (int s = 0; s < SMAX; ++s) {
+      if (s < steps) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16x16x32(a[u], b[u][mt], acc[mt]);
+        for (int mt = 0; mt < MT; ++mt) {
+          float h8[8], r8[8];
+          unpack8(hf[s][mt], h8);
+          unpack8(rf[s][mt], r8);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float r = h8[j] + r8[j];
+            ss[mt] = fmaf(r, r, ss[mt]);
+          }
+          if (a.residual_out && blockIdx.x == 0 && xok[mt]) {
+            float s8[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s8[j] = h8[j] + r8[j];
+            *reinterpret_cast<bf16x8*>(a.residual_out +
+                                       (int64_t)(mt * 16 + l16) * a.ro_stride + k_begin + s * 32) =
+                pack8(s8);
+          }
+        }
+      }
+    }
+    // Row sums over the four lane groups, then over the four wavefronts.
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      ss[mt] = xrow_sum(ss[mt]);
+      if (lg == 0) ssq[wave][mt][l16] = ss[mt];
+    }
+    __syncthreads();
+    float inv[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      inv[mt] = rsqrtf((ssq[0][mt][l16] + ssq[1][mt][l16] + ssq[2][mt][l16] +
+                        ssq[3][mt][l16]) / (float)a.K + a.eps);
+#pragma unroll
+    for (int s0 = 0; s0 < SMAX; s0 += kGemmBatch) {
+      if (s0 >= steps) break;
+      if (s0 > 0) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int u = 0; u < kGemmBatch; ++u)
+            if (s0 + u < steps)
+              wa[p][u] = *reinterpret_cast<const bf16x8*>(wrow[p] + (s0 + u) * 32);
+      }
+#pragma unroll
+      for (int u = 0; u < kGemmBatch; ++u) {
+        const int s = s0 + u;
+        if (s < steps && s < SMAX) {
+          float w8[8];
+          unpack8(*reinterpret_cast<const bf16x8*>(a.norm_w + k_begin + s * 32), w8);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            float h8[8], r8[8], x8[8];
+            unpack8(hf[s][mt], h8);
+            unpack8(rf[s][mt], r8);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x8[j] = (h8[j] + r8[j]) * inv[mt] * w8[j];
+            const bf16x8 xb = xok[mt] ? pack8(x8) : bf16x8{};
+#pragma unroll
+            for (int p = 0; p < NP; ++p) acc[p][mt] = mfma16x16x32(wa[p][u], xb, acc[p][mt]);
+          }
+        }
+      }
+    }
+  } else {
+    for (int s0 = 0; s0 < steps; s0 += kGemmBatch) {
+      bf16x8 wa[NP][kGemmBatch];
+      bf16x8 b[kGemmBatch][MT];
+#pragma unroll
+      for (int u = 0; u < kGemmBatch; ++u) {
+        if (s0 + u < steps) {
+#pragma unroll
+          for (int p = 0; p < NP; ++p)
+            wa[p][u] = *reinterpret_cast<const bf16x8*>(wrow[p] + (s0 + u) * 32);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            b[u][mt] = xok[mt] ? *reinterpret_cast<const bf16x8*>(a.x + xoff[mt] + (s0 + u) * 32)
+                               : bf16x8{};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kGemmBatch; ++u) {
+        if (s0 + u < steps) {
+#pragma unroll
+          for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              acc[p][mt] = mfma16x16x32(wa[p][u], b[u][mt], acc[p][mt]);
+        }
       }
     }
   }
 
-  // acc[mt][i] = y[m = mt*16 + l16][n = n0 + lg*4 + i] (partial over this K quarter)
+  // acc[p][mt][i] = y_p[m = mt*16 + l16][n = n0 + lg*4 + i] (partial over this K quarter)
   if (wave > 0) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) red[wave - 1][mt][lane] = acc[mt];
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[wave - 1][p][mt][lane] = acc[p][mt];
   }
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    f32x4 v = acc[mt] + red[0][mt][lane] + red[1][mt][lane] + red[2][mt][lane];
+    f32x4 v[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+      v[p] = acc[p][mt] + red[0][p][mt][lane] + red[1][p][mt][lane] + red[2][p][mt][lane];
     if (!xok[mt]) continue;
+    f32x4 o = v[0];
+    if constexpr (EPI == kSiluPair) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float g = round_bf16(v[0][i]);
+        const float u = round_bf16(v[NP - 1][i]);
+        o[i] = round_bf16(g / (1.f + expf(-g))) * u;
+      }
+    }
     uint2 packed;
-    packed.x = pack_bf16x2(v[0], v[1]);
-    packed.y = pack_bf16x2(v[2], v[3]);
-    *reinterpret_cast<uint2*>(y + (int64_t)(mt * 16 + l16) * y_stride + n0 + lg * 4) = packed;
+    packed.x = pack_bf16x2(o[0], o[1]);
+    packed.y = pack_bf16x2(o[2], o[3]);
+    *reinterpret_cast<uint2*>(a.y + (int64_t)(mt * 16 + l16) * a.y_stride + n0 + lg * 4) = packed;
   }
+}
+
+template <int PRO, int EPI>
+hipError_t launch_pe(const LinearArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)(a.N / 16));
+  switch ((a.M + 15) / 16) {
+    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI>), grid, dim3(kGemmThreads), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<2, PRO, EPI>), grid, dim3(kGemmThreads), 0, stream, a); break;
+    case 3: hipLaunchKernelGGL((skinny_gemm_kernel<3, PRO, EPI>), grid, dim3(kGemmThreads), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((skinny_gemm_kernel<4, PRO, EPI>), grid, dim3(kGemmThreads), 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -90,23 +257,18 @@ bool skinny_gemm_supported(int64_t M, int64_t N, int64_t K) {
          N / 16 <= 0x7fffffff;
 }
 
-hipError_t skinny_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_stride, void* y,
-                       int64_t y_stride, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-  const dim3 grid((unsigned)(N / 16));
-  const int mt = (int)((M + 15) / 16);
-#define AIOS_SKINNY(MT)                                                                         \
-  hipLaunchKernelGGL(skinny_gemm_kernel<MT>, grid, dim3(kGemmThreads), 0, stream,               \
-                     static_cast<const bf16*>(x), x_stride, static_cast<const bf16*>(w), w_stride, \
-                     static_cast<bf16*>(y), y_stride, (int)M, (int)K)
-  switch (mt) {
-    case 1: AIOS_SKINNY(1); break;
-    case 2: AIOS_SKINNY(2); break;
-    case 3: AIOS_SKINNY(3); break;
-    case 4: AIOS_SKINNY(4); break;
-    default: return hipErrorInvalidValue;
-  }
-#undef AIOS_SKINNY
-  return hipGetLastError();
+bool skinny_gemm_norm_supported(int64_t M, int64_t K) {
+  const int64_t mt = (M + 15) / 16;
+  return mt >= 1 && mt <= 4 && (K / 4) / 32 <= kNormMaxFrags / mt;
+}
+
+hipError_t skinny_gemm(const LinearArgs& a, int prologue, int epilogue, hipStream_t stream) {
+  if (prologue == kPlain && epilogue == kStore) return launch_pe<kPlain, kStore>(a, stream);
+  if (prologue == kPlain && epilogue == kSiluPair) return launch_pe<kPlain, kSiluPair>(a, stream);
+  if (prologue == kAddNorm && epilogue == kStore) return launch_pe<kAddNorm, kStore>(a, stream);
+  if (prologue == kAddNorm && epilogue == kSiluPair)
+    return launch_pe<kAddNorm, kSiluPair>(a, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace aios

@@ -107,9 +107,29 @@ hipError_t qk_norm_rope(const void* qkv, int64_t stride, int64_t tokens, int hq,
 hipError_t silu_mul(const void* x, int64_t x_stride, int64_t rows, int inter, void* out,
                     int64_t out_stride, hipStream_t stream);
 
+// Few-row GEMM y = x W^T with an optional prologue producing x and an
+// optional epilogue (see gemm_skinny.hip): prologue 0 plain, 1 residual-add
+// RMSNorm; epilogue 0 store, 1 SiLU of the gate half times the up half.
+struct LinearArgs {
+  const bf16* x;
+  int64_t x_stride;
+  const bf16* w;  // [N][K], or [2N][K] (gate rows, then up rows) for the SiLU pair
+  int64_t w_stride;
+  bf16* y;        // [M][N]
+  int64_t y_stride;
+  int32_t M;
+  int32_t K;
+  int64_t N;
+  const bf16* residual;  // prologue 1 (may be null)
+  int64_t r_stride;
+  const bf16* norm_w;    // prologue 1
+  float eps;
+  bf16* residual_out;    // prologue 1: bf16(x + residual) (may be null)
+  int64_t ro_stride;
+};
 bool skinny_gemm_supported(int64_t M, int64_t N, int64_t K);
-hipError_t skinny_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_stride, void* y,
-                       int64_t y_stride, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+bool skinny_gemm_norm_supported(int64_t M, int64_t K);
+hipError_t skinny_gemm(const LinearArgs& a, int prologue, int epilogue, hipStream_t stream);
 
 hipError_t greedy_select(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
                          int32_t elem_bytes, int64_t* token_out, float* logprob_out,

@@ -44,6 +44,45 @@ class HipOps:
         return y
 
     @staticmethod
+    def _rows_ok(x: torch.Tensor, weight: torch.Tensor, k: int) -> bool:
+        return (x.shape[0] <= 64 and weight.shape[0] % 16 == 0 and k % 128 == 0
+                and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+                and x.stride(1) == 1 and weight.stride(1) == 1 and x.stride(0) % 8 == 0
+                and weight.stride(0) % 8 == 0 and x.shape[0] > 0)
+
+    def add_rmsnorm_linear(self, h: torch.Tensor, residual: torch.Tensor | None,
+                           norm_weight: torch.Tensor, eps: float, weight: torch.Tensor,
+                           silu: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+        """RMSNormFused then a projection (norm.py:24-40): returns
+        (linear(RMSNorm(h + residual) * w), h + residual); with no residual the
+        new residual is h itself.  silu=True: weight is the merged gate/up
+        matrix and the projection is followed by silu_and_mul
+        (activation.py:9-12)."""
+        rows, k = h.shape
+        n = weight.shape[0] // 2 if silu else weight.shape[0]
+        if self._rows_ok(h, weight, k) and n % 16 == 0 and \
+                ((k // 4) // 32) * ((rows + 15) // 16) <= 8 and \
+                (residual is None or (residual.stride(1) == 1 and residual.stride(0) % 8 == 0)):
+            y = torch.empty(rows, n, dtype=h.dtype, device=h.device)
+            new_res = torch.empty_like(h) if residual is not None else h
+            _lib.check(_lib.lib().aios_linear_rows_ex(
+                h.data_ptr(), h.stride(0), weight.data_ptr(), weight.stride(0), y.data_ptr(),
+                y.stride(0), rows, n, k, _lib.PROLOGUE_ADD_RMSNORM,
+                residual.data_ptr() if residual is not None else None,
+                residual.stride(0) if residual is not None else 0, norm_weight.data_ptr(), eps,
+                new_res.data_ptr() if residual is not None else None,
+                new_res.stride(0) if residual is not None else 0,
+                _lib.EPILOGUE_SILU_MUL if silu else _lib.EPILOGUE_NONE, _stream(h)),
+                "aios_linear_rows_ex")
+            return y, new_res
+        if residual is None:
+            x, residual = self.rmsnorm(h, norm_weight, eps), h
+        else:  # (the inputs are left unchanged, as on the folded path)
+            x, residual = self.fused_add_rmsnorm(h.clone(), residual.clone(), norm_weight, eps)
+        y = self.linear(x, weight)
+        return (self.silu_and_mul(y) if silu else y), residual
+
+    @staticmethod
     def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
         _check_rows(x, "x")
         out = torch.empty_like(x)

@@ -73,8 +73,8 @@ class RotaryEmbedding:
 class Qwen3ForCausalLM:
     """Decoder + tied LM head.  ``forward()`` reads the batch from the global
     context like the reference (qwen3.py:140-173).  ``ops`` supplies linear,
-    rmsnorm, fused_add_rmsnorm, qk_norm_rope and silu_and_mul (default: the
-    gfx950 kernels, aios_amd.layers.HipOps)."""
+    add_rmsnorm_linear and qk_norm_rope (default: the gfx950 kernels,
+    aios_amd.layers.HipOps)."""
 
     def __init__(self, config: ModelConfig, weights: dict, device,
                  attn_backend: BaseAttentionBackend | None = None,
@@ -94,13 +94,13 @@ class Qwen3ForCausalLM:
         self._q_size = config.num_qo_heads * config.head_dim
         self._kv_size = config.num_kv_heads * config.head_dim
 
-    def _attention(self, i: int, h: torch.Tensor, positions, kv_cache, batch) -> torch.Tensor:
-        """qwen3.py:52-75: qkv projection, per-head q/k RMSNorm + RoPE, the
-        backend, o_proj (v stays a strided view into qkv, as in the reference)."""
+    def _attention(self, i: int, qkv: torch.Tensor, positions, kv_cache, batch) -> torch.Tensor:
+        """qwen3.py:52-75 after the qkv projection: per-head q/k RMSNorm +
+        RoPE, the backend, o_proj (v stays a strided view into qkv, as in the
+        reference)."""
         c = self.config
         lw = self.w["layers"][i]
-        t = h.shape[0]
-        qkv = self.ops.linear(h, lw["qkv"])
+        t = qkv.shape[0]
         q, k = self.ops.qk_norm_rope(qkv, lw["q_norm"], lw["k_norm"], self.rotary.cos,
                                      self.rotary.sin, positions, c.num_qo_heads, c.num_kv_heads,
                                      c.head_dim, c.rms_norm_eps)
@@ -109,6 +109,10 @@ class Qwen3ForCausalLM:
         return self.ops.linear(out.reshape(t, -1), lw["o"])
 
     def forward(self) -> torch.Tensor:
+        """Decoder layers of qwen3.py:76-109: input RMSNormFused -> qkv
+        projection, attention, post RMSNormFused -> gate/up projection ->
+        SiLU-and-mul, down projection; each norm is folded into the projection
+        that consumes it and the activation into the gate/up projection."""
         ctx = get_global_ctx()
         batch = ctx.batch
         c = self.config
@@ -117,15 +121,15 @@ class Qwen3ForCausalLM:
         positions = batch.positions
         residual = None
         for i, lw in enumerate(self.w["layers"]):
-            if residual is None:
-                residual = h
-                x = ops.rmsnorm(h, lw["input_norm"], c.rms_norm_eps)
-            else:
-                x, residual = ops.fused_add_rmsnorm(h, residual, lw["input_norm"], c.rms_norm_eps)
-            x = self._attention(i, x, positions, ctx.kv_cache, batch)
-            x, residual = ops.fused_add_rmsnorm(x, residual, lw["post_norm"], c.rms_norm_eps)
-            h = ops.linear(ops.silu_and_mul(ops.linear(x, lw["gate_up"])), lw["down"])
-        x, _ = ops.fused_add_rmsnorm(h, residual, self.w["final_norm"], c.rms_norm_eps)
+            qkv, residual = ops.add_rmsnorm_linear(h, residual, lw["input_norm"], c.rms_norm_eps,
+                                                   lw["qkv"])
+            x = self._attention(i, qkv, positions, ctx.kv_cache, batch)
+            act, residual = ops.add_rmsnorm_linear(x, residual, lw["post_norm"], c.rms_norm_eps,
+                                                   lw["gate_up"], silu=True)
+            h = ops.linear(act, lw["down"])
         if batch.is_prefill and not batch.return_all_logits:
-            x = x[batch.attn_metadata.get_last_indices(batch.size)]
-        return ops.linear(x, self.w["embed"])
+            last = batch.attn_metadata.get_last_indices(batch.size)
+            h, residual = h[last], residual[last]
+        logits, _ = ops.add_rmsnorm_linear(h, residual, self.w["final_norm"], c.rms_norm_eps,
+                                           self.w["embed"])
+        return logits

@@ -257,6 +257,32 @@ int aios_linear_rows(const void* x, int64_t x_stride, const void* weight, int64_
                      void* y, int64_t y_stride, int64_t rows, int64_t out_features,
                      int64_t in_features, void* stream);
 
+#define AIOS_PROLOGUE_NONE 0
+#define AIOS_PROLOGUE_ADD_RMSNORM 1
+#define AIOS_EPILOGUE_NONE 0
+#define AIOS_EPILOGUE_SILU_MUL 1
+
+/*
+ * aios_linear_rows with the ops around the projection folded in (same shape
+ * limits):
+ *   prologue AIOS_PROLOGUE_ADD_RMSNORM: the operand is bf16(RMSNorm(x +
+ *     residual) * norm_weight) as aios_rmsnorm computes it (residual may be
+ *     NULL), and residual_out (if not NULL; must not alias x or residual)
+ *     receives bf16(x + residual) -- RMSNormFused.forward followed by the
+ *     projection (python/aios/layers/norm.py:24-40, models/qwen3.py:
+ *     112-130); supported for in_features / 128 * ceil(rows / 16) <= 8;
+ *   epilogue AIOS_EPILOGUE_SILU_MUL: weight holds 2 * out_features rows
+ *     (gate rows, then up rows: the merged gate/up projection) and
+ *     y = silu_and_mul of the two bf16 halves
+ *     (python/aios/layers/activation.py:9-12, models/qwen3.py:91-93).
+ */
+int aios_linear_rows_ex(const void* x, int64_t x_stride, const void* weight, int64_t w_stride,
+                        void* y, int64_t y_stride, int64_t rows, int64_t out_features,
+                        int64_t in_features, int32_t prologue, const void* residual,
+                        int64_t residual_stride, const void* norm_weight, float eps,
+                        void* residual_out, int64_t residual_out_stride, int32_t epilogue,
+                        void* stream);
+
 /*
  * Greedy selection over rows of logits (elem_bytes 2: bf16, 4: fp32):
  *   token_out[r]   = first index of the maximum of logits[r, 0 .. vocab)

@@ -94,3 +94,46 @@ def test_linear_rows_strided_input_and_fallback():
     x65 = _bf16((65, 768), 7)  # more rows than the kernel takes: library GEMM
     torch.testing.assert_close(HipOps().linear(x65, w).float(), (x65.float() @ w.float().T),
                                atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("rows,k,n", [(1, 768, 1152), (8, 768, 1152), (8, 768, 6400),
+                                      (24, 1024, 512), (40, 512, 256), (8, 2048, 768)])
+@pytest.mark.parametrize("with_residual", [True, False])
+def test_add_rmsnorm_linear(rows, k, n, with_residual):
+    """RMSNorm (with the residual add) folded into the projection: the same
+    normalised operand as the separate kernels, the residual sum bit-exact."""
+    h = _bf16((rows, k), rows + k, 2.0)
+    r = _bf16((rows, k), rows + k + 1, 3.0) if with_residual else None
+    nw = _bf16((k,), 9).abs() + 0.5
+    w = _bf16((n, k), n, 0.05)
+    y, new_r = HipOps().add_rmsnorm_linear(h, r, nw, 1e-6, w)
+    ref = TorchOps()
+    if with_residual:
+        x_ref, r_ref = ref.fused_add_rmsnorm(h.clone(), r.clone(), nw, 1e-6)
+        assert torch.equal(new_r, r_ref)
+    else:
+        x_ref = ref.rmsnorm(h, nw, 1e-6)
+        assert new_r is h
+    y_ref = x_ref.float() @ w.float().T
+    err = (y.float() - y_ref).abs()
+    assert bool((err <= 2.0 ** -7 * y_ref.abs() + 2e-3 * y_ref.abs().max()).all()), err.max().item()
+
+
+@pytest.mark.parametrize("rows,k,inter", [(8, 768, 2048), (3, 512, 256), (33, 256, 512),
+                                          (1, 1024, 3072)])
+@pytest.mark.parametrize("with_residual", [True, False])
+def test_add_rmsnorm_linear_silu_pair(rows, k, inter, with_residual):
+    """Norm folded in front of the merged gate/up projection and SiLU-and-mul
+    behind it: matches norm -> GEMM (bf16 store) -> silu_and_mul."""
+    h = _bf16((rows, k), rows + k, 2.0)
+    r = _bf16((rows, k), rows + k + 1, 3.0) if with_residual else None
+    nw = _bf16((k,), 9).abs() + 0.5
+    w = _bf16((2 * inter, k), inter, 0.05)
+    y, _ = HipOps().add_rmsnorm_linear(h, r, nw, 1e-6, w, silu=True)
+    ref = TorchOps()
+    x_ref = (ref.fused_add_rmsnorm(h.clone(), r.clone(), nw, 1e-6)[0] if with_residual
+             else ref.rmsnorm(h, nw, 1e-6))
+    gu = (x_ref.float() @ w.float().T).to(torch.bfloat16)
+    y_ref = ref.silu_and_mul(gu).float()
+    err = (y.float() - y_ref).abs()
+    assert bool((err <= 2.0 ** -6 * y_ref.abs() + 4e-3 * y_ref.abs().max()).all()), err.max().item()

@@ -61,3 +61,12 @@ class TorchOps:
 
     def linear(self, x, weight):
         return torch.nn.functional.linear(x, weight)
+
+    def add_rmsnorm_linear(self, h, residual, norm_weight, eps, weight, silu=False):
+        if residual is None:
+            x = self.rmsnorm(h, norm_weight, eps)
+            residual = h
+        else:
+            x, residual = self.fused_add_rmsnorm(h.clone(), residual.clone(), norm_weight, eps)
+        y = self.linear(x, weight)
+        return (self.silu_and_mul(y) if silu else y), residual
