@@ -176,21 +176,35 @@ struct TileEngine {
     auto issue = [&](int s) {
       uint8_t* buf = lds + (s & (kRing - 1)) * T::SUB_BYTES;
       const int pos0 = kv_begin + s * kSubTok;
+      // All page-id reads first: every LDS DMA rewrites M0, which waits for
+      // outstanding LDS instructions, so reads interleaved with the DMAs
+      // would each pay a full LDS round trip.
+      uint32_t page[T::LPS];
 #pragma unroll
       for (int j = 0; j < T::LPS; ++j) {
         const int gp = pos0 + tok_j[j];
-        const uint32_t page = gp < kv_end ? (uint32_t)ids[gp - win] : 0xffffffffu;
-        const uint8_t* src = page < n_pages
-                                 ? (isv_j[j] ? vc : kc) + (page * tok_b + coff_j[j])
+        page[j] = gp < kv_end ? (uint32_t)ids[gp - win] : 0xffffffffu;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < T::LPS; ++j) {
+        const uint8_t* src = page[j] < n_pages
+                                 ? (isv_j[j] ? vc : kc) + (page[j] * tok_b + coff_j[j])
                                  : g_zero_kv_row + coff_j[j];
         __builtin_amdgcn_global_load_lds(
             src, (AIOS_LDS void*)(buf + (j * kEngineThreads + wave_u * 64) * 16), 16, 0, 0);
       }
     };
 
+    // The lookahead sub-tiles are issued unconditionally (those past the
+    // range gather the zero row into ring slots nobody reads), so one wait
+    // with a fixed count covers the Q loads and sub-tile 0 on every path.
+    // The compiler then sees Q complete before the loop; with Q possibly
+    // still in flight it would wait for every outstanding DMA (vmcnt(0))
+    // before each sub-tile's first MFMA and serialise the ring.
 #pragma unroll
-    for (int s = 0; s < kRing - 1; ++s)
-      if (s < n_sub) issue(s);
+    for (int s = 0; s < kRing - 1; ++s) issue(s);
+    wait_vmcnt<(kRing - 2) * T::LPS>();
 
     for (int it = 0; it < n_sub; ++it) {
       const int pend = min(kRing - 2, n_sub - 1 - it);

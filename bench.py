@@ -17,7 +17,9 @@ full-model CandidateGroup Top-3 latency of the MiniMind-0.1B-shaped model
 (``candidate_group``: p50/p95 over 30 seeded prefixes after 5 warmups, with
 graph-replayed and eager decode steps), and the reference's CPU attention
 path (restated, oracle/sdpa_cpu.py) timed on a bounded sample on the host
-cores.  ``roofline.traffic`` is the HBM bytes per launch measured with
+cores, and the causal prefill of the 4096-token prefix (``prefill``: one
+layer, TFLOP/s against the MFMA bf16 peak).  ``roofline.traffic`` is the HBM
+bytes per launch measured with
 rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by a plain-copy
 calibration), read from profiles/traffic.json.
 """
@@ -118,6 +120,48 @@ def cpu_baseline(wl, max_seconds: float) -> dict:
                    f"(oracle/sdpa_cpu.py), median of {len(times)} after 3 warmups, x{shape.num_layers}; "
                    f"cpu={_cpu_model()}, os.cpu_count={os.cpu_count()}"),
     }
+
+
+def prefix_prefill(seed: int, reps: int = 10) -> dict:
+    """Prefill of the long-context prefix: one layer of the Qwen3-4B-shaped
+    stack (32q/8kv heads of 128) over a 4096-token prompt whose pages are
+    scattered over a 65,536-page pool, causal, timed with HIP events over
+    `reps` back-to-back launches.  FLOPs = 4*Hq*D*q(q+1)/2 (QK^T and PV of
+    the causal triangle)."""
+    import torch
+
+    from aios_amd import paged
+
+    dev = torch.device("cuda:0")
+    t, hq, hkv, d, pages = 4096, 32, 8, 128, 65536
+    g = torch.Generator(device=dev).manual_seed(seed)
+    kc = (torch.randn(pages, hkv, d, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    vc = (torch.randn(pages, hkv, d, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    q = (torch.randn(t, hq, d, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    idx = torch.randperm(pages, generator=g, device=dev)[:t].to(torch.int32)
+    cu_q = torch.tensor([0, t], dtype=torch.int32)
+    p = paged.plan("prefill", cu_q, cu_q, hq, hkv, d)
+    out = torch.empty_like(q)
+    cu = cu_q.to(dev)
+    s = torch.cuda.Stream(dev)
+    with torch.cuda.stream(s):
+        paged.prefill(p, q, kc, vc, idx, cu, cu, out=out)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            paged.prefill(p, q, kc, vc, idx, cu, cu, out=out)
+        e1.record(s)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    flops = 4 * hq * d * t * (t + 1) / 2
+    tflops = flops / us / 1e6
+    del kc, vc, q, out
+    torch.cuda.empty_cache()
+    return {"workload": "causal prefill, 4096 tokens, 32q/8kv D128, scattered pages, one layer",
+            "kernel": "prefill_kernel<128>", "avg_launch_us": round(us, 2),
+            "flop_per_launch": int(flops), "bound": "mfma", "achieved": round(tflops, 1),
+            "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4)}
 
 
 def candidate_group(seed: int, runs: int = 30, warmups: int = 5) -> dict:
@@ -364,6 +408,8 @@ def main() -> int:
     del wl, out, ws, ws2, k_new, v_new, main_calls, comb_calls, graph
     torch.cuda.empty_cache()
     _log(f"decode step {ms_per_step * 1e3:.1f} us; main kernel {casc_ms * 1e3:.2f} us")
+    result["prefill"] = prefix_prefill(args.seed)
+    _log(f"prefix prefill {result['prefill']['avg_launch_us']} us")
     if not args.no_candidate_group:
         result["candidate_group"] = candidate_group(args.seed)
         _log(f"candidate group {result['candidate_group']['graph']['top3_p50_ms']} ms p50")
