@@ -30,6 +30,8 @@
 // python/aios/attention/flashinfer.py:33-91 (decode: q_len 1).
 #pragma once
 
+#include <type_traits>
+
 #include "kernels.hpp"
 
 #define AIOS_LDS __attribute__((address_space(3)))
@@ -59,6 +61,29 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   asm volatile("s_barrier" ::: "memory");
+}
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 (LDS transpose read) as inline asm.  The compiler
+// treats the builtin's read as possibly aliasing any LDS DMA in flight and
+// waits for all of them (vmcnt(0)) before it, which would stall every
+// sub-tile on the DMAs just issued for later ring slots; the ring protocol
+// (explicit vmcnt waits, then a barrier) already orders each sub-tile's DMA
+// before its reads.  The compiler does not count the asm read in lgkmcnt:
+// lds_wait_tied waits for it with the results as operands, so no use of them
+// can be scheduled above the wait.
+__device__ __forceinline__ bf16x4 lds_read_tr(const uint8_t* p) {
+  const uint32_t addr = (uint32_t)(uintptr_t)(AIOS_LDS const uint8_t*)p;
+  uint64_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return __builtin_bit_cast(bf16x4, r);
+}
+__device__ __forceinline__ void lds_wait_tied(bf16x4& a, bf16x4& b) {
+  uint64_t x = __builtin_bit_cast(uint64_t, a), y = __builtin_bit_cast(uint64_t, b);
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x), "+v"(y));
+  a = __builtin_bit_cast(bf16x4, x);
+  b = __builtin_bit_cast(bf16x4, y);
 }
 
 template <int D>
@@ -179,12 +204,11 @@ struct TileEngine {
       // All page-id reads first: every LDS DMA rewrites M0, which waits for
       // outstanding LDS instructions, so reads interleaved with the DMAs
       // would each pay a full LDS round trip.
+      // Positions past kv_end read the -1 that stage_ids left there (the
+      // window always covers the sub-tile, lookahead sub-tiles included).
       uint32_t page[T::LPS];
 #pragma unroll
-      for (int j = 0; j < T::LPS; ++j) {
-        const int gp = pos0 + tok_j[j];
-        page[j] = gp < kv_end ? (uint32_t)ids[gp - win] : 0xffffffffu;
-      }
+      for (int j = 0; j < T::LPS; ++j) page[j] = (uint32_t)ids[pos0 + tok_j[j] - win];
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < T::LPS; ++j) {
@@ -206,28 +230,37 @@ struct TileEngine {
     for (int s = 0; s < kRing - 1; ++s) issue(s);
     wait_vmcnt<(kRing - 2) * T::LPS>();
 
-    for (int it = 0; it < n_sub; ++it) {
-      const int pend = min(kRing - 2, n_sub - 1 - it);
-      if (pend >= 2)
-        wait_vmcnt<2 * T::LPS>();
-      else if (pend == 1)
-        wait_vmcnt<T::LPS>();
-      else
-        wait_vmcnt<0>();
-      lds_barrier();  // sub-tile `it` is in LDS; every wave is done with it-1
-      const int s_next = it + kRing - 1;
-      if (s_next < n_sub) {
-        if (kv_begin + s_next * kSubTok >= win + kIdWindow) {
-          win += kIdWindow;
-          stage_ids();
-          lds_barrier();
+    // The loop is instantiated twice so that no branch around the math
+    // sits inside it: a conditional compute makes the accumulators phi
+    // values, and the compiler then copies every O tile once per sub-tile.
+    auto loop = [&](auto with_math) {
+      for (int it = 0; it < n_sub; ++it) {
+        const int pend = min(kRing - 2, n_sub - 1 - it);
+        if (pend >= 2)
+          wait_vmcnt<2 * T::LPS>();
+        else if (pend == 1)
+          wait_vmcnt<T::LPS>();
+        else
+          wait_vmcnt<0>();
+        lds_barrier();  // sub-tile `it` is in LDS; every wave is done with it-1
+        const int s_next = it + kRing - 1;
+        if (s_next < n_sub) {
+          if (kv_begin + s_next * kSubTok >= win + kIdWindow) {
+            win += kIdWindow;
+            stage_ids();
+            lds_barrier();
+          }
+          issue(s_next);
         }
-        issue(s_next);
+        if constexpr (decltype(with_math)::value)
+          compute(lds + (it & (kRing - 1)) * T::SUB_BYTES, kv_begin + it * kSubTok, kv_end,
+                  scale_log2, l16, lg);
       }
-      if (active)
-        compute(lds + (it & (kRing - 1)) * T::SUB_BYTES, kv_begin + it * kSubTok, kv_end,
-                scale_log2, l16, lg);
-    }
+    };
+    if (__builtin_amdgcn_readfirstlane((int)active))
+      loop(std::true_type{});
+    else
+      loop(std::false_type{});
     finish();
   }
 
@@ -242,7 +275,6 @@ struct TileEngine {
   __device__ __forceinline__ void compute(const uint8_t* kb, int kv0, int kv_end, float scale_log2,
                                           int l16, int lg) {
     const uint8_t* vb = kb + T::SUB_KB;
-    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
     // Issue every LDS operand read of the sub-tile before the first MFMA so
     // their latencies overlap: K rows (A of S^T) and the V^T fragments (A of
     // O^T, transpose reads; consumed after the softmax).
@@ -266,10 +298,8 @@ struct TileEngine {
         const int dim = dt * 16 + 4 * q4;
         const int c = dim >> 3;
         const int boff = (dim & 7) * 2;
-        va[dt][0] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (AIOS_LDS bf16x4*)(vb + t0 * T::ROWB + T::v_slot(t0, c) * 16 + boff));
-        va[dt][1] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (AIOS_LDS bf16x4*)(vb + t1 * T::ROWB + T::v_slot(t1, c) * 16 + boff));
+        va[dt][0] = lds_read_tr(vb + t0 * T::ROWB + T::v_slot(t0, c) * 16 + boff);
+        va[dt][1] = lds_read_tr(vb + t1 * T::ROWB + T::v_slot(t1, c) * 16 + boff);
       }
     }
     // S^T tiles: st[rt][tt][i] = S[row rt*16 + l16][token tt*16 + lg*4 + i];
@@ -310,8 +340,8 @@ struct TileEngine {
             if (!ok) x[rt][tt * 4 + i] = kNegInf;
           }
       }
-      mx[rt] = fmaxf(fmaxf(fmaxf(x[rt][0], x[rt][1]), fmaxf(x[rt][2], x[rt][3])),
-                     fmaxf(fmaxf(x[rt][4], x[rt][5]), fmaxf(x[rt][6], x[rt][7])));
+      mx[rt] = vmax(vmax(vmax(x[rt][0], x[rt][1]), vmax(x[rt][2], x[rt][3])),
+                    vmax(vmax(x[rt][4], x[rt][5]), vmax(x[rt][6], x[rt][7])));
     }
     bool need[RT];
     bool any = false;
@@ -353,6 +383,8 @@ struct TileEngine {
     // O^T += V^T P^T.  Lane (lg, l16) supplied V[token][dt*16 + 4*(l16%4)..+3]
     // of tokens lg*4 + l16/4 (first read) and 16 + lg*4 + l16/4 (second read)
     // and received V[tokens][dt*16 + l16], the A fragment rows of the MFMA.
+#pragma unroll
+    for (int dt = 0; dt < DTILES; ++dt) lds_wait_tied(va[dt][0], va[dt][1]);
 #pragma unroll
     for (int dt = 0; dt < DTILES; ++dt) {
       const bf16x8 vf = __builtin_shufflevector(va[dt][0], va[dt][1], 0, 1, 2, 3, 4, 5, 6, 7);
