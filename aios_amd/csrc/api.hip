@@ -30,7 +30,8 @@ int32_t cdiv(int32_t a, int32_t b) { return (a + b - 1) / b; }
 
 // Shared prefixes shorter than this are read per row (no second launch).
 constexpr int32_t kMinCascadePrefix = 128;
-// Partial states per (row, kv-head) the combine merges.
+// Partial states per (row, kv-head) the combine merges (one per lane of a
+// wavefront when it computes the merge weights).
 constexpr int32_t kMaxParts = 64;
 
 // Compute units of the current device, looked up once per process (host

@@ -6,19 +6,19 @@
 //     one chunk of the shared prefix for one kv-head and up to 128 of the
 //     batch*G query rows; the prefix KV is therefore read once per kv-head
 //     for the whole group, not once per candidate;
-//   * suffix workgroups: four wavefronts, each owning one (row, kv-head,
-//     split) item of the row's own pages after the prefix.  The 64 lanes form
-//     four 16-lane DPP rows; each DPP row takes every fourth KV position and
-//     each lane holds D/16 dims, so a q.k dot product is a per-lane partial
-//     sum plus a 4-step DPP row reduction.  All page-id loads of the item are
-//     issued together, then all K/V loads, so one item costs two memory
-//     latencies rather than one per position.
+//   * suffix workgroups: one (row, kv-head, split) item of the row's own
+//     pages after the prefix.  Its four wavefronts take the item's
+//     32-position sub-tiles round-robin, gather each into their own LDS
+//     region and run the tile engine's math with one 16-row MFMA tile
+//     holding the row's G query heads; the four softmax states are merged
+//     through LDS.  With k_new / v_new given, the row's new token is read
+//     from them and written to its page in the same launch.
 // Every workgroup writes a normalised partial (o, lse) into the parts array
 // (layout in kernels.hpp); decode_combine_kernel merges the parts of each
-// (row, kv-head) with m = max lse_j, w_j = 2^(lse_j - m),
-// out = sum w_j o_j / sum w_j (the split/merge rule of online softmax,
+// (row, kv-head) with m = max lse_j, w_j = 2^(lse_j - m) / sum_i 2^(lse_i - m),
+// out = sum w_j o_j (the split/merge rule of online softmax,
 // resources/lesson-41-flashattention-online-softmax/run_lesson41.py:7-18).
-// When a (row, head) has a single part the suffix wavefront writes bf16
+// When a (row, head) has a single part the suffix workgroup writes bf16
 // output directly and no combine runs.
 #include "engine.hpp"
 
@@ -256,6 +256,9 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
 template <int D, int G>
 __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_main_kernel(DecodeArgs a) {
   __shared__ __align__(16) uint8_t lds[KVTile<D>::LDS_BYTES];
+  // Prefix workgroups first: they carry most of the bytes, and dispatching
+  // the suffix items ahead of them measured slower (their loads delay the
+  // prefix streaming more than the suffix items gain).
   const int wg = blockIdx.x;
   if (wg < a.prefix_wgs) {
     decode_prefix_part<D>(lds, a, wg);
@@ -267,20 +270,37 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
 // ---------------------------------------------------------------------------
 // combine: one workgroup per (row, kv-head)
 constexpr int kCombineThreads = 256;
-constexpr int kCombineMaxParts = 64;
-constexpr int kCombineBatch = 32;  // parts whose o loads one thread keeps in flight
+constexpr int kCombineMaxParts = 64;  // one part per lane of a wavefront
+constexpr int kCombineBatch = 32;     // parts whose o loads one thread keeps in flight
+
+// Max / sum over the 64 lanes of a wavefront (DPP inside 16-lane rows, then
+// the lane swaps across rows); every lane receives the result.
+__device__ __forceinline__ float wave_max(float x) {
+  int v;
+  v = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false);
+  x = vmax(x, __int_as_float(v));
+  v = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false);
+  x = vmax(x, __int_as_float(v));
+  v = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false);
+  x = vmax(x, __int_as_float(v));
+  v = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false);
+  x = vmax(x, __int_as_float(v));
+  return xrow_max(x);
+}
+__device__ __forceinline__ float wave_sum(float x) { return xrow_sum(row16_sum(x)); }
 
 template <int D, int G>
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeArgs a) {
   constexpr int E4 = G * D / 4;  // float4 elements per part
   static_assert(E4 <= kCombineThreads, "one float4 per thread per part");
   constexpr int R = kCombineThreads / E4;  // threads sharing one element
-  __shared__ float lse_s[kCombineMaxParts * G];
-  __shared__ float mx_s[G];
-  __shared__ float den_s[G];
+  constexpr int NW = kCombineThreads / 64;
+  __shared__ float w_s[kCombineMaxParts * G];
   __shared__ f32x4 red[kCombineThreads];
 
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int bh = blockIdx.x;
   const int b = bh / a.num_kv_heads;
   const int h = bh - b * a.num_kv_heads;
@@ -299,33 +319,29 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
   const uint2* po =
       reinterpret_cast<const uint2*>(a.parts.o + a.parts.o_index(D, h, 0, row, d));
 
-  // Issue this thread's o loads first (independent of the weights).
+  // This thread's o loads go out first (they do not depend on the weights).
   uint2 v[kCombineBatch];
 #pragma unroll
   for (int k = 0; k < kCombineBatch; ++k) {
     const int j = r + k * R;
     v[k] = (active && j < np) ? po[(int64_t)j * part_stride / 4] : make_uint2(0, 0);
   }
-  for (int i = tid; i < np * G; i += kCombineThreads)
-    lse_s[i] = a.parts.lse[a.parts.lse_index(h, i / G, b * G + i % G)];
-  __syncthreads();
-  if (tid < G) {
-    float mx = kNegInf;
-    for (int j = 0; j < np; ++j) mx = fmaxf(mx, lse_s[j * G + tid]);
+  // Normalised weights w_j = 2^(lse_j - m) / sum_i 2^(lse_i - m),
+  // m = max_j lse_j: one wavefront per query row, lane j = part j.
+  for (int gg = wave; gg < G; gg += NW) {
+    const float l = lane < np ? a.parts.lse[a.parts.lse_index(h, lane, b * G + gg)] : kNegInf;
+    const float mx = wave_max(l);
     const float mu = (mx == kNegInf) ? 0.f : mx;
-    float den = 0.f;
-    for (int j = 0; j < np; ++j) den += fast_exp2(lse_s[j * G + tid] - mu);
-    mx_s[tid] = mu;
-    den_s[tid] = den;
+    const float w = lane < np ? fast_exp2(l - mu) : 0.f;
+    const float den = wave_sum(w);
+    if (lane < np) w_s[lane * G + gg] = den > 0.f ? w / den : 0.f;
   }
   __syncthreads();
 
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   if (active) {
-    const float mu = mx_s[g];
     auto fold = [&](int j, uint2 w) {
-      const float f = fast_exp2(lse_s[j * G + g] - mu);
-      acc += f32x4{lo_bf16(w.x), hi_bf16(w.x), lo_bf16(w.y), hi_bf16(w.y)} * f;
+      acc += f32x4{lo_bf16(w.x), hi_bf16(w.x), lo_bf16(w.y), hi_bf16(w.y)} * w_s[j * G + g];
     };
 #pragma unroll
     for (int k = 0; k < kCombineBatch; ++k) {
@@ -352,11 +368,9 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
       for (int rr = 1; rr < R; ++rr) acc += red[rr * E4 + e];
   }
   if (active && r == 0) {
-    const float den = den_s[g];
-    const f32x4 res = den > 0.f ? acc * (1.f / den) : f32x4{0.f, 0.f, 0.f, 0.f};
     uint2 packed;
-    packed.x = pack_bf16x2(res[0], res[1]);
-    packed.y = pack_bf16x2(res[2], res[3]);
+    packed.x = pack_bf16x2(acc[0], acc[1]);
+    packed.y = pack_bf16x2(acc[2], acc[3]);
     *reinterpret_cast<uint2*>(a.out + ((int64_t)b * a.num_qo_heads + h * G + g) * D + d) = packed;
   }
 }
