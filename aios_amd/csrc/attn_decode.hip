@@ -291,12 +291,14 @@ __device__ __forceinline__ float wave_sum(float x) { return xrow_sum(row16_sum(x
 
 template <int D, int G>
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeArgs a) {
-  constexpr int E4 = G * D / 4;  // float4 elements per part
-  static_assert(E4 <= kCombineThreads, "one float4 per thread per part");
-  constexpr int R = kCombineThreads / E4;  // threads sharing one element
+  constexpr int E8 = G * D / 8;  // 8-dim (16-byte) elements per part
+  static_assert(E8 <= kCombineThreads, "one element per thread per part");
+  constexpr int R = kCombineThreads / E8;  // threads sharing one element (parts split)
   constexpr int NW = kCombineThreads / 64;
+  constexpr int PB = (kCombineMaxParts + R - 1) / R;  // parts per thread, upper bound
+  constexpr int BATCH = PB < kCombineBatch ? PB : kCombineBatch;
   __shared__ float w_s[kCombineMaxParts * G];
-  __shared__ f32x4 red[kCombineThreads];
+  __shared__ f32x4 red[kCombineThreads][2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -305,73 +307,84 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeA
   const int b = bh / a.num_kv_heads;
   const int h = bh - b * a.num_kv_heads;
   const int np = a.parts.n_parts;
-  const int e = tid % E4;
-  const int r = tid / E4;
-  const bool active = r < R;
-  // Element e = 4 dims of one row: dims dt*16 + q4*4 .. +3 of head g, so
-  // consecutive threads read the G adjacent rows of one 16-dim tile.
-  const int q4 = e & 3;
-  const int g = (e >> 2) % G;
-  const int dt = e / (4 * G);
-  const int d = dt * 16 + q4 * 4;
+  const int e = tid % E8;
+  const int r = tid / E8;
+  const bool active = r < R;  // G * D / 8 need not divide the workgroup
+  // Element e = 8 dims of one row: dims dt*16 + q8*8 .. +7 of head g, so
+  // consecutive threads read the G adjacent rows of one 16-dim tile
+  // (G * 32 contiguous bytes of a part).
+  const int q8 = e & 1;
+  const int g = (e >> 1) % G;
+  const int dt = e / (2 * G);
+  const int d = dt * 16 + q8 * 8;
   const int row = b * G + g;
   const int64_t part_stride = (int64_t)(D / 16) * a.parts.rows * 16;  // elements per part
-  const uint2* po =
-      reinterpret_cast<const uint2*>(a.parts.o + a.parts.o_index(D, h, 0, row, d));
+  const uint4* po = reinterpret_cast<const uint4*>(a.parts.o + a.parts.o_index(D, h, 0, row, d));
 
-  // This thread's o loads go out first (they do not depend on the weights).
-  uint2 v[kCombineBatch];
+  // The lse loads go out first, so the weights below wait only for them;
+  // then this thread's o loads (parts r, r + R, ...).
+  constexpr int LG = (G + NW - 1) / NW;  // query rows per wavefront
+  float l[LG];
 #pragma unroll
-  for (int k = 0; k < kCombineBatch; ++k) {
+  for (int i = 0; i < LG; ++i) {
+    const int gg = i * NW + wave;
+    l[i] = gg < G && lane < np ? a.parts.lse[a.parts.lse_index(h, lane, b * G + gg)] : kNegInf;
+  }
+  uint4 v[BATCH];
+#pragma unroll
+  for (int k = 0; k < BATCH; ++k) {
     const int j = r + k * R;
-    v[k] = (active && j < np) ? po[(int64_t)j * part_stride / 4] : make_uint2(0, 0);
+    v[k] = active && j < np ? po[(int64_t)j * part_stride / 8] : make_uint4(0, 0, 0, 0);
   }
   // Normalised weights w_j = 2^(lse_j - m) / sum_i 2^(lse_i - m),
-  // m = max_j lse_j: one wavefront per query row, lane j = part j.
-  for (int gg = wave; gg < G; gg += NW) {
-    const float l = lane < np ? a.parts.lse[a.parts.lse_index(h, lane, b * G + gg)] : kNegInf;
-    const float mx = wave_max(l);
-    const float mu = (mx == kNegInf) ? 0.f : mx;
-    const float w = lane < np ? fast_exp2(l - mu) : 0.f;
-    const float den = wave_sum(w);
-    if (lane < np) w_s[lane * G + gg] = den > 0.f ? w / den : 0.f;
+  // m = max_j lse_j: one wavefront per query row, lane j = part j (zero for
+  // lanes past the last part).
+#pragma unroll
+  for (int i = 0; i < LG; ++i) {
+    const int gg = i * NW + wave;
+    if (gg < G) {  // uniform per wavefront
+      const float mx = wave_max(l[i]);
+      const float mu = (mx == kNegInf) ? 0.f : mx;
+      const float w = lane < np ? fast_exp2(l[i] - mu) : 0.f;
+      const float den = wave_sum(w);
+      w_s[lane * G + gg] = den > 0.f ? w / den : 0.f;
+    }
   }
   __syncthreads();
 
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (active) {
-    auto fold = [&](int j, uint2 w) {
-      acc += f32x4{lo_bf16(w.x), hi_bf16(w.x), lo_bf16(w.y), hi_bf16(w.y)} * w_s[j * G + g];
-    };
+  f32x4 acc0 = f32x4{0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+  auto fold = [&](int j, const uint4& x) {
+    const float w = w_s[j * G + g];
+    acc0 += f32x4{lo_bf16(x.x), hi_bf16(x.x), lo_bf16(x.y), hi_bf16(x.y)} * w;
+    acc1 += f32x4{lo_bf16(x.z), hi_bf16(x.z), lo_bf16(x.w), hi_bf16(x.w)} * w;
+  };
+  // Parts past the last one hold zeros and weight zero (j < kCombineMaxParts
+  // keeps every w_s read in bounds).
 #pragma unroll
-    for (int k = 0; k < kCombineBatch; ++k) {
-      const int j = r + k * R;
-      if (j < np) fold(j, v[k]);
+  for (int k = 0; k < BATCH; ++k) fold(min(r + k * R, kCombineMaxParts - 1), v[k]);
+  for (int j0 = r + BATCH * R; active && j0 < np; j0 += BATCH * R) {
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) {
+      const int j = j0 + k * R;
+      v[k] = j < np ? po[(int64_t)j * part_stride / 8] : make_uint4(0, 0, 0, 0);
     }
-    for (int j0 = r + kCombineBatch * R; j0 < np; j0 += kCombineBatch * R) {
 #pragma unroll
-      for (int k = 0; k < kCombineBatch; ++k) {
-        const int j = j0 + k * R;
-        v[k] = j < np ? po[(int64_t)j * part_stride / 4] : make_uint2(0, 0);
-      }
-#pragma unroll
-      for (int k = 0; k < kCombineBatch; ++k) {
-        const int j = j0 + k * R;
-        if (j < np) fold(j, v[k]);
-      }
-    }
+    for (int k = 0; k < BATCH; ++k) fold(min(j0 + k * R, kCombineMaxParts - 1), v[k]);
   }
   if (R > 1) {
-    red[tid] = acc;
+    red[tid][0] = acc0;
+    red[tid][1] = acc1;
     __syncthreads();
-    if (active && r == 0)
-      for (int rr = 1; rr < R; ++rr) acc += red[rr * E4 + e];
+    if (r == 0)
+      for (int rr = 1; rr < R; ++rr) {
+        acc0 += red[rr * E8 + e][0];
+        acc1 += red[rr * E8 + e][1];
+      }
   }
   if (active && r == 0) {
-    uint2 packed;
-    packed.x = pack_bf16x2(acc[0], acc[1]);
-    packed.y = pack_bf16x2(acc[2], acc[3]);
-    *reinterpret_cast<uint2*>(a.out + ((int64_t)b * a.num_qo_heads + h * G + g) * D + d) = packed;
+    const uint4 packed = make_uint4(pack_bf16x2(acc0[0], acc0[1]), pack_bf16x2(acc0[2], acc0[3]),
+                                    pack_bf16x2(acc1[0], acc1[1]), pack_bf16x2(acc1[2], acc1[3]));
+    *reinterpret_cast<uint4*>(a.out + ((int64_t)b * a.num_qo_heads + h * G + g) * D + d) = packed;
   }
 }
 
