@@ -270,15 +270,14 @@ struct TileEngine {
     for (int rt = 0; rt < RT; ++rt) l_run[rt] = xrow_sum(l_run[rt]);
   }
 
-  // One 32-token sub-tile in LDS (KVTile layout) for the lane's RT rows;
-  // positions >= kv_end (and, if CAUSAL, past each row's limit) are masked.
-  __device__ __forceinline__ void compute(const uint8_t* kb, int kv0, int kv_end, float scale_log2,
-                                          int l16, int lg) {
-    const uint8_t* vb = kb + T::SUB_KB;
-    // Issue every LDS operand read of the sub-tile before the first MFMA so
-    // their latencies overlap: K rows (A of S^T) and the V^T fragments (A of
-    // O^T, transpose reads; consumed after the softmax).
-    bf16x8 kf[2][KSTEPS];
+  // The math of one 32-token sub-tile in LDS (KVTile layout) for the lane's
+  // RT rows, in steps; positions >= kv_end (and, if CAUSAL, past each row's
+  // limit) are masked.  (Deferring each sub-tile's O^T update into the next
+  // iteration, behind the next S^T MFMAs, measured no faster.)
+
+  // K rows (A of S^T = K Q^T), B = the Q fragments in registers.
+  __device__ __forceinline__ void read_k(const uint8_t* kb, bf16x8 (&kf)[2][KSTEPS], int l16,
+                                         int lg) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       const int t = tt * 16 + l16;
@@ -287,24 +286,11 @@ struct TileEngine {
         kf[tt][s] = *reinterpret_cast<const bf16x8*>(kb + t * T::ROWB +
                                                       T::k_slot(t, s * 4 + lg) * 16);
     }
-    bf16x4 va[DTILES][2];
-    {
-      const int r = l16 >> 2;
-      const int q4 = l16 & 3;
-      const int t0 = lg * 4 + r;
-      const int t1 = 16 + lg * 4 + r;
-#pragma unroll
-      for (int dt = 0; dt < DTILES; ++dt) {
-        const int dim = dt * 16 + 4 * q4;
-        const int c = dim >> 3;
-        const int boff = (dim & 7) * 2;
-        va[dt][0] = lds_read_tr(vb + t0 * T::ROWB + T::v_slot(t0, c) * 16 + boff);
-        va[dt][1] = lds_read_tr(vb + t1 * T::ROWB + T::v_slot(t1, c) * 16 + boff);
-      }
-    }
-    // S^T tiles: st[rt][tt][i] = S[row rt*16 + l16][token tt*16 + lg*4 + i];
-    // the accumulation chains are interleaved.
-    f32x4 st[RT][2];
+  }
+
+  // S^T tiles: st[rt][tt][i] = S[row rt*16 + l16][token tt*16 + lg*4 + i];
+  // the accumulation chains are interleaved.
+  __device__ __forceinline__ void mma_s(const bf16x8 (&kf)[2][KSTEPS], f32x4 (&st)[RT][2]) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -316,10 +302,34 @@ struct TileEngine {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
           st[rt][tt] = mfma16x16x32(kf[tt][s], qf[rt][s], st[rt][tt]);
+  }
 
-    // Online softmax with a lazily moved reference: m_run only moves when a
-    // row's scaled max exceeds it by more than kRescaleSlack (p <= 2^slack
-    // otherwise), so the O rescale below is skipped once the max settles.
+  // V^T fragments (A of O^T += V^T P^T) by LDS transpose reads: lane
+  // (lg, l16) supplies V[token][dt*16 + 4*(l16%4)..+3] of tokens
+  // lg*4 + l16/4 (first read) and 16 + lg*4 + l16/4 (second read) and
+  // receives V[tokens][dt*16 + l16], the A fragment rows of the MFMA.
+  __device__ __forceinline__ void load_v(const uint8_t* vb, bf16x4 (&va)[DTILES][2], int l16,
+                                         int lg) {
+    const int r = l16 >> 2;
+    const int q4 = l16 & 3;
+    const int t0 = lg * 4 + r;
+    const int t1 = 16 + lg * 4 + r;
+#pragma unroll
+    for (int dt = 0; dt < DTILES; ++dt) {
+      const int dim = dt * 16 + 4 * q4;
+      const int c = dim >> 3;
+      const int boff = (dim & 7) * 2;
+      va[dt][0] = lds_read_tr(vb + t0 * T::ROWB + T::v_slot(t0, c) * 16 + boff);
+      va[dt][1] = lds_read_tr(vb + t1 * T::ROWB + T::v_slot(t1, c) * 16 + boff);
+    }
+  }
+
+  // Online softmax with a lazily moved reference: m_run only moves when a
+  // row's scaled max exceeds it by more than kRescaleSlack (p <= 2^slack
+  // otherwise), so the O rescale below is skipped once the max settles.
+  // P (bf16, the B operand of the O^T MFMA) goes to pb.
+  __device__ __forceinline__ void softmax(const f32x4 (&st)[RT][2], int kv0, int kv_end,
+                                          float scale_log2, int lg, bf16x8 (&pb)[RT]) {
     const bool full = kv0 + kSubTok <= kv_end && (!CAUSAL || kv0 + kSubTok - 1 <= min_limit);
     float x[RT][8];
     float mx[RT];
@@ -363,7 +373,6 @@ struct TileEngine {
         m_run[rt] = need[rt] ? mx[rt] : m_run[rt];
       }
     }
-    bf16x8 pb[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const float m_use = (m_run[rt] == kNegInf) ? 0.f : m_run[rt];
@@ -379,10 +388,10 @@ struct TileEngine {
           bf16x8, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
                              pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])));
     }
+  }
 
-    // O^T += V^T P^T.  Lane (lg, l16) supplied V[token][dt*16 + 4*(l16%4)..+3]
-    // of tokens lg*4 + l16/4 (first read) and 16 + lg*4 + l16/4 (second read)
-    // and received V[tokens][dt*16 + l16], the A fragment rows of the MFMA.
+  // O^T += V^T P^T.
+  __device__ __forceinline__ void accumulate(bf16x4 (&va)[DTILES][2], const bf16x8 (&pb)[RT]) {
 #pragma unroll
     for (int dt = 0; dt < DTILES; ++dt) lds_wait_tied(va[dt][0], va[dt][1]);
 #pragma unroll
@@ -391,6 +400,21 @@ struct TileEngine {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) o[rt][dt] = mfma16x16x32(vf, pb[rt], o[rt][dt]);
     }
+  }
+
+  // All four steps on one sub-tile, every LDS read issued before the first
+  // MFMA.
+  __device__ __forceinline__ void compute(const uint8_t* kb, int kv0, int kv_end, float scale_log2,
+                                          int l16, int lg) {
+    bf16x8 kf[2][KSTEPS];
+    bf16x4 va[DTILES][2];
+    f32x4 st[RT][2];
+    bf16x8 pb[RT];
+    read_k(kb, kf, l16, lg);
+    load_v(kb + T::SUB_KB, va, l16, lg);
+    mma_s(kf, st);
+    softmax(st, kv0, kv_end, scale_log2, lg, pb);
+    accumulate(va, pb);
   }
 };
 
