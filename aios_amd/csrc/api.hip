@@ -207,10 +207,16 @@ static int check_plan(const aios_attn_plan_t* p, int phase) {
   return AIOS_OK;
 }
 
+// The attention kernels address one layer's K (or V) cache with 32-bit byte
+// offsets (buffer descriptors), so a layer's cache must stay below 4 GiB.
 static int check_cache(int64_t kv_num_pages, int64_t tok_stride) {
   if (kv_num_pages < 0) return fail(AIOS_ERR_INVALID, "negative page count");
+  const int64_t bytes = kv_num_pages * tok_stride * 2;
+  if (bytes > 0xffff0000ll)
+    return fail(AIOS_ERR_UNSUPPORTED,
+                "per-layer KV cache of %lld bytes exceeds the 4 GiB the kernels address",
+                (long long)bytes);
   return AIOS_OK;
-  (void)tok_stride;
 }
 
 int aios_attn_prefill(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,

@@ -45,8 +45,11 @@ constexpr int kEngineThreads = 256;
 // The softmax reference may lag a row's running max by up to 2^8.
 constexpr float kRescaleSlack = 8.0f;
 
-// Source of every masked / out-of-range K or V chunk.
+// Source of every masked / out-of-range K or V chunk of the suffix gathers.
 static __device__ __align__(16) uint8_t g_zero_kv_row[512] = {0};
+
+// Word 3 of a raw buffer descriptor on gfx9-family GPUs (32-bit data format).
+constexpr int kBufferWord3 = 0x00020000;
 
 // s_waitcnt with vmcnt <= N and the other counters unconstrained.
 template <int N>
@@ -179,16 +182,19 @@ struct TileEngine {
 
     // Loop-invariant part of every DMA load of this thread: which token of
     // the sub-tile it serves, and the byte offset (rotated chunk) inside that
-    // token's K or V row.  Per-layer caches are below 4 GiB, so page offsets
-    // are 32-bit.
+    // token's K or V row.  Whether load j of a wavefront fills K or V rows is
+    // uniform over the wavefront (the K part of a sub-tile is a whole number
+    // of 1 KiB wavefront loads), so it selects a buffer descriptor held in
+    // scalar registers.
+    static_assert(T::SUB_KB % (64 * 16) == 0, "K part of a sub-tile in whole wavefront loads");
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     int tok_j[T::LPS];
     uint32_t coff_j[T::LPS];
     bool isv_j[T::LPS];
 #pragma unroll
     for (int j = 0; j < T::LPS; ++j) {
+      const bool isv = (j * kEngineThreads + wave_u * 64) * 16 >= T::SUB_KB;
       const int off = (j * kEngineThreads + tid) * 16;
-      const bool isv = off >= T::SUB_KB;
       const int o2 = isv ? off - T::SUB_KB : off;
       const int t = o2 / T::ROWB;
       const int slot = (o2 - t * T::ROWB) >> 4;
@@ -196,8 +202,18 @@ struct TileEngine {
       isv_j[j] = isv;
       coff_j[j] = (uint32_t)((isv ? T::v_chunk(t, slot) : T::k_chunk(t, slot)) * 16);
     }
+    // Raw buffer descriptors over this head's K and V rows: the last valid
+    // byte is the end of the last page's row, so a page id clamped to
+    // num_pages lands past it and the load returns zeros (the hardware range
+    // check); the host keeps a layer's cache below 4 GiB so offsets are 32-bit.
     const uint32_t tok_b = (uint32_t)tok_bytes;
     const uint32_t n_pages = (uint32_t)num_pages;
+    const int64_t n_rec64 = num_pages > 0 ? (num_pages - 1) * tok_bytes + T::ROWB : 0;
+    const int n_rec = (int)(n_rec64 < 0xffffffffll ? n_rec64 : 0xffffffffll);
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)kc, (short)0, n_rec, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)vc, (short)0, n_rec, kBufferWord3);
     auto issue = [&](int s) {
       uint8_t* buf = lds + (s & (kRing - 1)) * T::SUB_BYTES;
       const int pos0 = kv_begin + s * kSubTok;
@@ -212,11 +228,10 @@ struct TileEngine {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < T::LPS; ++j) {
-        const uint8_t* src = page[j] < n_pages
-                                 ? (isv_j[j] ? vc : kc) + (page[j] * tok_b + coff_j[j])
-                                 : g_zero_kv_row + coff_j[j];
-        __builtin_amdgcn_global_load_lds(
-            src, (AIOS_LDS void*)(buf + (j * kEngineThreads + wave_u * 64) * 16), 16, 0, 0);
+        const uint32_t off = min(page[j], n_pages) * tok_b + coff_j[j];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            isv_j[j] ? rv : rk, (AIOS_LDS void*)(buf + (j * kEngineThreads + wave_u * 64) * 16),
+            16, off, 0, 0, 0);
       }
     };
 

@@ -286,3 +286,22 @@ def test_append_decode_rejects_new_token_inside_shared_prefix():
                             wl.k_cache[0].to(DEV), wl.v_cache[0].to(DEV), wl.indices.to(DEV),
                             wl.cu_k.to(DEV), workspace=torch.empty(1 << 20, dtype=torch.uint8,
                                                                    device=DEV))
+
+
+def test_layer_cache_above_4gib_is_rejected():
+    """The kernels address a layer's cache with 32-bit byte offsets: a page
+    count that puts the cache at 4 GiB is refused before any launch."""
+    from aios_amd import _lib
+
+    wl = make_decode_workload(OP_TEST, seed=3)
+    out, p = _run(wl)
+    q = wl.q[0].to(DEV)
+    kc = wl.k_cache[0].to(DEV)
+    ws = torch.empty(max(p.ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    pages = (1 << 32) // (p.num_kv_heads * p.head_dim * 2)
+    status = _lib.lib().aios_attn_decode(
+        p, q.data_ptr(), q.stride(0), kc.data_ptr(), kc.data_ptr(), pages,
+        wl.indices.to(DEV).data_ptr(), wl.cu_k.to(DEV).data_ptr(), out.data_ptr(),
+        ws.data_ptr(), ws.numel(), p.head_dim ** -0.5, None)
+    assert status == _lib.AIOS_ERR_UNSUPPORTED
+    assert "4 GiB" in _lib.lib().aios_last_error().decode()
