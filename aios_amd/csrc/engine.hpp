@@ -119,7 +119,8 @@ struct TileEngine {
   bf16x8 qf[RT][KSTEPS];
   f32x4 o[RT][DTILES];
   float m_run[RT];
-  float l_run[RT];
+  float l_run[RT];  // row totals, set by finish()
+  f32x4 ol[RT];     // row sums of P by MFMA (every element holds the sum)
   int limit[RT];   // CAUSAL: last visible KV position of the lane's rows
   int min_limit;   // CAUSAL: smallest limit of any row of the workgroup
 
@@ -143,6 +144,7 @@ struct TileEngine {
       for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
       m_run[rt] = kNegInf;
       l_run[rt] = 0.f;
+      ol[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
 
@@ -279,10 +281,10 @@ struct TileEngine {
     finish();
   }
 
-  // Row totals across the four lane groups (after the last compute).
+  // Row totals (after the last compute).
   __device__ __forceinline__ void finish() {
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) l_run[rt] = xrow_sum(l_run[rt]);
+    for (int rt = 0; rt < RT; ++rt) l_run[rt] = ol[rt][0];
   }
 
   // The math of one 32-token sub-tile in LDS (KVTile layout) for the lane's
@@ -354,7 +356,7 @@ struct TileEngine {
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[rt][tt * 4 + i] = st[rt][tt][i];
-      if (!full) {
+      if (__builtin_expect(!full, 0)) {
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -382,7 +384,7 @@ struct TileEngine {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         const float al = need[rt] ? fast_exp2(m_run[rt] - mx[rt]) : 1.f;
-        l_run[rt] *= al;
+        ol[rt][0] *= al;  // the other elements of ol are never read
 #pragma unroll
         for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] *= al;
         m_run[rt] = need[rt] ? mx[rt] : m_run[rt];
@@ -392,21 +394,20 @@ struct TileEngine {
     for (int rt = 0; rt < RT; ++rt) {
       const float m_use = (m_run[rt] == kNegInf) ? 0.f : m_run[rt];
       float p[8];
-      float psum = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        p[j] = fast_exp2(fmaf(x[rt][j], scale_log2, -m_use));
-        psum += p[j];
-      }
-      l_run[rt] += psum;
+      for (int j = 0; j < 8; ++j) p[j] = fast_exp2(fmaf(x[rt][j], scale_log2, -m_use));
       pb[rt] = __builtin_bit_cast(
           bf16x8, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
                              pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])));
     }
   }
 
-  // O^T += V^T P^T.
+  // O^T += V^T P^T, and the row sums of P by one more MFMA with an all-ones
+  // A operand (the sum the O^T numerator sees, of the bf16 P).
   __device__ __forceinline__ void accumulate(bf16x4 (&va)[DTILES][2], const bf16x8 (&pb)[RT]) {
+    const bf16x8 ones = (bf16x8)(bf16)1.0f;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) ol[rt] = mfma16x16x32(ones, pb[rt], ol[rt]);
 #pragma unroll
     for (int dt = 0; dt < DTILES; ++dt) lds_wait_tied(va[dt][0], va[dt][1]);
 #pragma unroll
