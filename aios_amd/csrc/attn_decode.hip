@@ -106,6 +106,7 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   constexpr int NW = kEngineThreads / 64;
   constexpr int DT = D / 16;
   static_assert(CH % 64 == 0, "sub-tile must split over one wavefront");
+  static_assert((CH / 2) % 64 == 0, "each wavefront load is all K or all V");
   static_assert(G <= 16, "one MFMA row tile");
   static_assert(DT * 64 * 16 + 2 * 16 * 4 <= T::SUB_BYTES, "merge state fits the wave region");
   const int lane = threadIdx.x & 63;
@@ -169,12 +170,23 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
     uint32_t sel = kNoPage;
     if (lane < kSubTok && pos < s_end)
       sel = pos == t_new ? (new_ok ? kNewTok : kNoPage) : (uint32_t)a.indices[base + pos];
+    // Loads whose tokens all lie past the item's end are skipped (the math
+    // masks those tokens and zeroes their V fragments).
+    // All page-id exchanges first: each LDS DMA rewrites M0, which waits for
+    // outstanding LDS instructions, and a load behind the exchanges would
+    // also be waited for.
+    const int n_valid = __builtin_amdgcn_readfirstlane(min(s_end - kv0, kSubTok));
+    uint32_t page[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) page[j] = (uint32_t)__shfl((int)sel, tok_j[j]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const uint32_t page = (uint32_t)__shfl((int)sel, tok_j[j]);
-      const uint8_t* src = page < n_pages ? (isv_j[j] ? vc : kc) + (page * tok_b + coff_j[j])
-                           : page == kNewTok ? (isv_j[j] ? vn : kn) + coff_j[j]
-                                             : g_zero_kv_row + coff_j[j];
+      if (((j * 64) % (CH / 2)) / T::CPR >= n_valid) continue;
+      const uint8_t* src = page[j] < n_pages
+                               ? (isv_j[j] ? vc : kc) + (page[j] * tok_b + coff_j[j])
+                           : page[j] == kNewTok ? (isv_j[j] ? vn : kn) + coff_j[j]
+                                                : g_zero_kv_row + coff_j[j];
       __builtin_amdgcn_global_load_lds(src, (AIOS_LDS void*)(buf + j * 64 * 16), 16, 0, 0);
     }
     wait_vmcnt<0>();

@@ -403,13 +403,32 @@ struct TileEngine {
   }
 
   // O^T += V^T P^T, and the row sums of P by one more MFMA with an all-ones
-  // A operand (the sum the O^T numerator sees, of the bf16 P).
-  __device__ __forceinline__ void accumulate(bf16x4 (&va)[DTILES][2], const bf16x8 (&pb)[RT]) {
+  // A operand (the sum the O^T numerator sees, of the bf16 P).  V rows of
+  // tokens >= n_valid may be stale LDS (gathers that skip them): their
+  // fragments are zeroed so that P = 0 there cannot meet a NaN.
+  __device__ __forceinline__ void accumulate(bf16x4 (&va)[DTILES][2], const bf16x8 (&pb)[RT],
+                                             int n_valid, int lg) {
     const bf16x8 ones = (bf16x8)(bf16)1.0f;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) ol[rt] = mfma16x16x32(ones, pb[rt], ol[rt]);
 #pragma unroll
     for (int dt = 0; dt < DTILES; ++dt) lds_wait_tied(va[dt][0], va[dt][1]);
+    if (__builtin_expect(n_valid < kSubTok, 0)) {
+      // va[dt][tt] element i belongs to token tt*16 + lg*4 + i.
+      uint64_t keep[2];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        keep[tt] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (tt * 16 + lg * 4 + i < n_valid) keep[tt] |= 0xffffull << (16 * i);
+      }
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+          va[dt][tt] = __builtin_bit_cast(bf16x4, __builtin_bit_cast(uint64_t, va[dt][tt]) & keep[tt]);
+    }
 #pragma unroll
     for (int dt = 0; dt < DTILES; ++dt) {
       const bf16x8 vf = __builtin_shufflevector(va[dt][0], va[dt][1], 0, 1, 2, 3, 4, 5, 6, 7);
@@ -430,7 +449,7 @@ struct TileEngine {
     load_v(kb + T::SUB_KB, va, l16, lg);
     mma_s(kf, st);
     softmax(st, kv0, kv_end, scale_log2, lg, pb);
-    accumulate(va, pb);
+    accumulate(va, pb, kv_end - kv0, lg);
   }
 };
 
