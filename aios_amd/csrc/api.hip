@@ -339,10 +339,6 @@ int decode_impl(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
     a.v_new_stride = nk->v_stride;
     a.out_loc = nk->out_loc;
   }
-  {
-    const char* v = getenv("AIOS_EXP");
-    a.variant = v ? atoi(v) : 0;
-  }
   if (mask & 1) {
     rc = check_hip(aios::launch_decode_main(D, a, s), "decode launch");
     if (rc) return rc;

@@ -64,7 +64,6 @@ struct DecodeArgs {
   int64_t k_new_stride;  // elements per token
   int64_t v_new_stride;
   const int32_t* out_loc;
-  int32_t variant;
 };
 
 struct PrefillArgs {
