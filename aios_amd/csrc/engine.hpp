@@ -8,11 +8,12 @@
 //
 // Data movement: the range's page ids are staged in LDS, then K/V rows are
 // gathered page by page straight from HBM into an LDS ring of four 32-token
-// sub-tiles with global_load_lds_dwordx4 (no VGPR staging), three sub-tiles
-// ahead of the one being consumed.  Rows are stored token-major with the sixteen-byte
-// chunks of each row rotated (K by the token index, V by twice the token
-// index) so that both MFMA operand reads below are bank-conflict free.
-// Masked or out-of-range positions load a zero row.
+// sub-tiles with raw-buffer LDS loads (buffer_load_dwordx4 ... lds, no VGPR
+// staging), three sub-tiles ahead of the one being consumed.  Rows are
+// stored token-major with the sixteen-byte chunks of each row rotated by a
+// multiple of the token index (chosen per head size, see KVTile) so that
+// the MFMA operand reads below avoid LDS bank conflicts.  Masked or
+// out-of-range positions load a zero row.
 //
 // Math per 32-token sub-tile and wavefront:
 //   S^T = K Q^T         v_mfma_f32_16x16x32_bf16, A = K rows (ds_read_b128),
@@ -99,14 +100,24 @@ struct KVTile {
   static constexpr int RING_BYTES = kRing * SUB_BYTES;
   static constexpr int LDS_BYTES = RING_BYTES + kIdWindow * 4;
   static_assert(SUB_BYTES % (kEngineThreads * 16) == 0, "sub-tile must split evenly");
-  static_assert(4 * CPR >= kSubTok && 8 * CPR >= 2 * kSubTok, "rotation range");
 
-  // Chunk slot of (token t, chunk c) and its inverse.
-  static __device__ __forceinline__ int k_slot(int t, int c) { return (c + t) % CPR; }
-  static __device__ __forceinline__ int v_slot(int t, int c) { return (c + 2 * t) % CPR; }
-  static __device__ __forceinline__ int k_chunk(int t, int slot) { return (slot + 4 * CPR - t) % CPR; }
+  // Chunk c of token t's row sits in slot (c + rot(t)) % CPR of the row.
+  // The rotations were chosen by measuring LDS read rates on gfx950 (four
+  // wavefronts, the exact lane patterns of the reads below): K (read with
+  // ds_read_b128) conflict-free for D = 64 and 128 and at the best measured
+  // rate for D = 96; V (read with ds_read_b64_tr_b16) conflict-free.
+  static __device__ __forceinline__ int k_rot(int t) {
+    return D == 128 ? 2 * t : D == 96 ? t >> 1 : t;
+  }
+  static __device__ __forceinline__ int v_rot(int t) { return D == 128 ? t : 2 * t; }
+  static __device__ __forceinline__ int k_slot(int t, int c) { return (c + k_rot(t)) % CPR; }
+  static __device__ __forceinline__ int v_slot(int t, int c) { return (c + v_rot(t)) % CPR; }
+  // Inverses: which chunk a slot holds.
+  static __device__ __forceinline__ int k_chunk(int t, int slot) {
+    return (slot + CPR - k_rot(t) % CPR) % CPR;
+  }
   static __device__ __forceinline__ int v_chunk(int t, int slot) {
-    return (slot + 8 * CPR - 2 * t) % CPR;
+    return (slot + CPR - v_rot(t) % CPR) % CPR;
   }
 };
 
