@@ -149,6 +149,8 @@ int aios_attn_plan(int32_t phase, const int32_t* cu_q_host,
  * [kv_num_pages, Hkv, D] contiguous, out is [total_q, Hq, D] contiguous.
  * cu_q, cu_k and indices are device int32.  A page id outside
  * [0, kv_num_pages) is read as an all-zero K/V row (never dereferenced).
+ * One layer's cache (kv_num_pages * Hkv * D * 2 bytes) must be below 4 GiB
+ * (the kernels use 32-bit byte offsets); AIOS_ERR_UNSUPPORTED otherwise.
  */
 int aios_attn_prefill(const aios_attn_plan_t* plan, const void* q,
                       int64_t q_tok_stride, const void* k_cache,
@@ -163,7 +165,8 @@ int aios_attn_prefill(const aios_attn_plan_t* plan, const void* q,
  * indices[cu_k[b] + pos].  Positions [0, plan->prefix_len) are read through
  * row 0's page ids (indices[0 .. prefix_len)) once per kv-head and shared by
  * all rows; the rest are read per row.  workspace holds the partial softmax
- * states (plan->ws_bytes bytes).
+ * states (plan->ws_bytes bytes).  Page ids and the 4 GiB per-layer cache
+ * limit as for aios_attn_prefill.
  */
 int aios_attn_decode(const aios_attn_plan_t* plan, const void* q,
                      int64_t q_tok_stride, const void* k_cache,
