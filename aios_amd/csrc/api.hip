@@ -232,6 +232,8 @@ int aios_attn_prefill(const aios_attn_plan_t* p, const void* q, int64_t q_tok_st
                 (long long)q_tok_stride);
   if (!q || !k_cache || !v_cache || !indices || !cu_q || !cu_k || !out)
     return fail(AIOS_ERR_INVALID, "prefill: null pointer");
+  if ((((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) & 15) != 0)
+    return fail(AIOS_ERR_INVALID, "prefill: q, caches and out must be 16-byte aligned");
   if ((rc = check_cache(kv_num_pages, (int64_t)p->num_kv_heads * D))) return rc;
   aios::PrefillArgs a = {};
   a.q = static_cast<const aios::bf16*>(q);
@@ -284,6 +286,8 @@ int decode_impl(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
     return fail(AIOS_ERR_INVALID, "decode: workspace must be 256-byte aligned");
   if (!q || !k_cache || !v_cache || !indices || !cu_k || !out)
     return fail(AIOS_ERR_INVALID, "decode: null pointer");
+  if ((((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) & 15) != 0)
+    return fail(AIOS_ERR_INVALID, "decode: q, caches and out must be 16-byte aligned");
   if ((rc = check_cache(kv_num_pages, (int64_t)p->num_kv_heads * D))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);

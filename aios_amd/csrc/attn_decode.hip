@@ -245,23 +245,40 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
       acc[dt] += reinterpret_cast<const f32x4*>(lds + w * T::SUB_BYTES)[dt * 64 + lane] * f[w];
   }
 
-  if (l16 >= G) return;
+  // The G x D result is staged in LDS (wave 0's own region, free now) in
+  // the order of its destination and written with full-width 16-byte
+  // stores: one store instruction per 64 chunks instead of one per 16-dim
+  // tile from the G active lanes (store issue is slow while the CU's memory
+  // pipeline is full of the prefix gathers).
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  const int row = b * G + l16;
+  bf16* stage = reinterpret_cast<bf16*>(lds);
+  if (l16 < G) {
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    const f32x4 v = acc[dt] * inv;
-    uint2 packed;
-    packed.x = pack_bf16x2(v[0], v[1]);
-    packed.y = pack_bf16x2(v[2], v[3]);
-    bf16* dstp = a.final_out
-                     ? a.out + ((int64_t)b * a.num_qo_heads + h * G + l16) * D + dt * 16 + lg * 4
-                     : a.parts.o + a.parts.o_index(D, h, a.parts.n_chunks + split, row,
-                                                   dt * 16 + lg * 4);
-    *reinterpret_cast<uint2*>(dstp) = packed;
+    for (int dt = 0; dt < DT; ++dt) {
+      const f32x4 v = acc[dt] * inv;
+      const int e = a.final_out ? l16 * D + dt * 16 + lg * 4 : (dt * G + l16) * 16 + lg * 4;
+      *reinterpret_cast<uint2*>(stage + e) = make_uint2(pack_bf16x2(v[0], v[1]),
+                                                       pack_bf16x2(v[2], v[3]));
+    }
   }
-  if (!a.final_out && lg == 0)
-    a.parts.lse[a.parts.lse_index(h, a.parts.n_chunks + split, row)] =
+  // The same wavefront reads the staged rows back: its LDS accesses
+  // complete in order.
+  constexpr int NCH = G * D / 8;  // 16-byte chunks of the result
+  for (int c = lane; c < NCH; c += 64) {
+    const uint4 v = reinterpret_cast<const uint4*>(stage)[c];
+    bf16* dst;
+    if (a.final_out) {
+      dst = a.out + ((int64_t)b * a.num_qo_heads + h * G) * D + c * 8;
+    } else {
+      const int dt = c * 8 / (G * 16);
+      const int r = c * 8 - dt * G * 16;
+      dst = a.parts.o + a.parts.o_index(D, h, a.parts.n_chunks + split, b * G + r / 16,
+                                        dt * 16 + (r & 15));
+    }
+    *reinterpret_cast<uint4*>(dst) = v;
+  }
+  if (!a.final_out && lg == 0 && l16 < G)
+    a.parts.lse[a.parts.lse_index(h, a.parts.n_chunks + split, b * G + l16)] =
         l_tot > 0.f ? mx + fast_log2(l_tot) : kNegInf;
 }
 

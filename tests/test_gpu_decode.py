@@ -305,3 +305,16 @@ def test_layer_cache_above_4gib_is_rejected():
         ws.data_ptr(), ws.numel(), p.head_dim ** -0.5, None)
     assert status == _lib.AIOS_ERR_UNSUPPORTED
     assert "4 GiB" in _lib.lib().aios_last_error().decode()
+
+
+def test_misaligned_output_is_rejected():
+    """Kernels store 16-byte vectors: an output view 8 bytes off alignment is
+    refused with ValueError before any launch."""
+    wl = make_decode_workload(OP_TEST, seed=4)
+    out, p = _run(wl)
+    ws = torch.empty(max(p.ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    flat = torch.empty(out.numel() + 8, dtype=torch.bfloat16, device=DEV)
+    bad = flat[4:4 + out.numel()].view(out.shape)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        paged.decode(p, wl.q[0].to(DEV), wl.k_cache[0].to(DEV), wl.v_cache[0].to(DEV),
+                     wl.indices.to(DEV), wl.cu_k.to(DEV), out=bad, workspace=ws)
