@@ -15,7 +15,9 @@ Prints one JSON line: value = decode-step microseconds (lower is better),
 with the main decode kernel's roofline measured live with HIP events, the
 full-model CandidateGroup Top-3 latency of the MiniMind-0.1B-shaped model
 (``candidate_group``: p50/p95 over 30 seeded prefixes after 5 warmups, with
-graph-replayed and eager decode steps), and the reference's CPU attention
+graph-replayed and eager decode steps) and of the Qwen3-0.6B-shaped model
+on a 128-token prefix extended by 2 ids (``candidate_group_qwen3_0p6b``:
+the cross-keystroke case, 8 candidates x 24 steps), the reference's CPU attention
 path (restated, oracle/sdpa_cpu.py) timed on a bounded sample on the host
 cores, and the causal prefill of the 4096-token prefix (``prefill``: one
 layer, TFLOP/s against the MFMA bf16 peak).  ``roofline.traffic`` is the HBM
@@ -164,42 +166,51 @@ def prefix_prefill(seed: int, reps: int = 10) -> dict:
             "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4)}
 
 
-def candidate_group(seed: int, runs: int = 30, warmups: int = 5) -> dict:
-    """Full CandidateGroup Top-3 latency of the MiniMind-0.1B-shaped model.
+def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int = 32,
+                    steps: int = 16, extend: int = 0, runs: int = 30, warmups: int = 5) -> dict:
+    """Full CandidateGroup Top-3 latency of a synthetic-weight model.
 
-    14 layers, hidden 768, 8q/2kv heads of 96, SwiGLU 2048, vocab 6400, seeded
-    N(0, 0.02) bf16 weights.  One run = complete(): prefill a 32-token prefix
-    of seeded random ids, then 8 candidates x 16 greedy steps over the shared
-    prefix KV, Top-3 by average log-prob (the reference protocol of
-    bench_ime.py:75-76, 170-196 without text governance).  ``warmups`` runs on
-    other prefixes come first (the first one captures the decode-step graph);
-    each run starts from an empty prefix cache.
+    Default: the MiniMind-0.1B-shaped model (14 layers, hidden 768, 8q/2kv
+    heads of 96, SwiGLU 2048, vocab 6400), seeded N(0, 0.02) bf16 weights.
+    One run = complete(): prefill a `prefix_tokens` prefix of seeded random
+    ids, then 8 candidates x `steps` greedy steps over the shared prefix KV,
+    Top-3 by average log-prob (the reference protocol of bench_ime.py:75-76,
+    170-196 without text governance).  With `extend` > 0 (the cross-keystroke
+    case), each run first completes the prefix untimed and then times
+    complete() on the prefix extended by `extend` ids, which prefills only
+    those ids against the cached prefix KV (token-LCP reuse, ime.py:1116-1168).
+    ``warmups`` runs on other prefixes come first (the first one captures the
+    decode-step graph); each run starts from an empty prefix cache.
     """
     import statistics
 
     import torch
 
-    from aios_amd.config import MINIMIND_0P1B
+    from aios_amd.config import MODELS
     from aios_amd.core import reset_global_ctx
     from aios_amd.ime import CandidateGroupConfig, CandidateGroupEngine, CandidateGroupRuntime
     from aios_amd.qwen3 import init_weights
 
-    c = MINIMIND_0P1B
+    c = MODELS[model]
     rt = CandidateGroupRuntime(c, init_weights(c, seed, "cuda"), "cuda", num_pages=2048)
-    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=16)
-    out = {"model": "minimind-0.1b-shaped (14L, 768, 8q/2kv x 96, ffn 2048, vocab 6400)",
-           "prefix_tokens": 32, "candidates": 8, "decode_steps": 16, "runs": runs,
-           "warmups": warmups}
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=steps)
+    out = {"model": f"{model}-shaped ({c.num_layers}L, {c.hidden_size}, "
+                    f"{c.num_qo_heads}q/{c.num_kv_heads}kv x {c.head_dim}, "
+                    f"ffn {c.intermediate_size}, vocab {c.vocab_size})",
+           "prefix_tokens": prefix_tokens, "extend_tokens": extend, "candidates": 8,
+           "decode_steps": steps, "runs": runs, "warmups": warmups}
     for mode in ("graph", "eager"):
         eng = CandidateGroupEngine(rt, use_graphs=mode == "graph")
         lat, gpu, gen = [], [], 0
         first = None
         for i in range(warmups + runs):
             g = torch.Generator().manual_seed(seed + 1000 + i)
-            prefix = torch.randint(c.vocab_size, (32,), generator=g).tolist()
+            ids = torch.randint(c.vocab_size, (prefix_tokens + extend,), generator=g).tolist()
             eng.reset_prefix_cache()
+            if extend:
+                eng.complete(ids[:prefix_tokens], cfg)
             t0 = time.perf_counter()
-            r = eng.complete(prefix, cfg)
+            r = eng.complete(ids, cfg)
             dt = (time.perf_counter() - t0) * 1e3
             if first is None:
                 first = dt
@@ -413,6 +424,13 @@ def main() -> int:
     if not args.no_candidate_group:
         result["candidate_group"] = candidate_group(args.seed)
         _log(f"candidate group {result['candidate_group']['graph']['top3_p50_ms']} ms p50")
+        # Qwen3-0.6B-shaped: 128-token prefix extended by 2 ids (cross-keystroke
+        # reuse), 8 candidates x 24 steps.
+        result["candidate_group_qwen3_0p6b"] = candidate_group(
+            args.seed, model="qwen3-0.6b", prefix_tokens=128, steps=24, extend=2, runs=20,
+            warmups=3)
+        _log(f"candidate group qwen3-0.6b "
+             f"{result['candidate_group_qwen3_0p6b']['graph']['top3_p50_ms']} ms p50")
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cpu_wl, args.cpu_seconds)
         _log("cpu baseline done")
