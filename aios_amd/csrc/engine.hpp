@@ -9,7 +9,9 @@
 // Data movement: the range's page ids are staged in LDS, then K/V rows are
 // gathered page by page straight from HBM into an LDS ring of four 32-token
 // sub-tiles with raw-buffer LDS loads (buffer_load_dwordx4 ... lds, no VGPR
-// staging), three sub-tiles ahead of the one being consumed.  Rows are
+// staging), two sub-tiles ahead of the one being consumed (three measured
+// no faster: the decode launch is not bound by the stream depth, and a
+// shallower queue lets the suffix items' dependent loads through sooner).  Rows are
 // stored token-major with the sixteen-byte chunks of each row rotated by a
 // multiple of the token index (chosen per head size, see KVTile) so that
 // the MFMA operand reads below avoid LDS bank conflicts.  Masked or
@@ -41,6 +43,8 @@ namespace aios {
 
 constexpr int kSubTok = 32;       // KV positions per sub-tile
 constexpr int kRing = 4;          // sub-tiles in the LDS ring
+constexpr int kLookahead = 2;     // sub-tiles in flight ahead of the one consumed (< kRing)
+static_assert(kLookahead < kRing, "the slot being consumed is never refilled");
 constexpr int kIdWindow = 1024;   // page ids staged in LDS at a time
 constexpr int kEngineThreads = 256;
 // The softmax reference may lag a row's running max by up to 2^8.
@@ -255,15 +259,15 @@ struct TileEngine {
     // still in flight it would wait for every outstanding DMA (vmcnt(0))
     // before each sub-tile's first MFMA and serialise the ring.
 #pragma unroll
-    for (int s = 0; s < kRing - 1; ++s) issue(s);
-    wait_vmcnt<(kRing - 2) * T::LPS>();
+    for (int s = 0; s < kLookahead; ++s) issue(s);
+    wait_vmcnt<(kLookahead - 1) * T::LPS>();
 
     // The loop is instantiated twice so that no branch around the math
     // sits inside it: a conditional compute makes the accumulators phi
     // values, and the compiler then copies every O tile once per sub-tile.
     auto loop = [&](auto with_math) {
       for (int it = 0; it < n_sub; ++it) {
-        const int pend = min(kRing - 2, n_sub - 1 - it);
+        const int pend = min(kLookahead - 1, n_sub - 1 - it);
         if (pend >= 2)
           wait_vmcnt<2 * T::LPS>();
         else if (pend == 1)
@@ -271,7 +275,7 @@ struct TileEngine {
         else
           wait_vmcnt<0>();
         lds_barrier();  // sub-tile `it` is in LDS; every wave is done with it-1
-        const int s_next = it + kRing - 1;
+        const int s_next = it + kLookahead;
         if (s_next < n_sub) {
           if (kv_begin + s_next * kSubTok >= win + kIdWindow) {
             win += kIdWindow;
