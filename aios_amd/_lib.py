@@ -70,7 +70,7 @@ class AttnPlan(ctypes.Structure):
         ("num_q_tiles", ctypes.c_int32),
         ("stage_mask", ctypes.c_int32),
         ("min_kv_len", ctypes.c_int32),
-        ("reserved0", ctypes.c_int32),
+        ("suffix_parts_per_item", ctypes.c_int32),
         ("ws_parts_o", ctypes.c_int64),
         ("ws_parts_lse", ctypes.c_int64),
         ("ws_bytes", ctypes.c_int64),

@@ -177,7 +177,14 @@ int aios_attn_plan(int32_t phase, const int32_t* cu_q, const int32_t* cu_k, int3
       n_chunks = cdiv(P, chunk);
     }
   }
-  const int32_t n_parts = n_chunks + n_splits;
+  // With the cascade the combine runs anyway: each suffix wavefront then
+  // writes its own part instead of merging the item's four states through
+  // LDS first (the merge waits for the slowest wavefront and then runs on
+  // one), as long as the part count stays within the bound.
+  const int32_t per_item =
+      (cascade && n_chunks + n_splits * aios::kSuffixWaves <= kMaxParts) ? aios::kSuffixWaves : 1;
+  const int32_t n_parts = n_chunks + n_splits * per_item;
+  p->suffix_parts_per_item = per_item;
   p->prefix_len = P;
   p->prefix_chunk_len = chunk;
   p->num_prefix_chunks = n_chunks;
@@ -317,6 +324,7 @@ int decode_impl(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
   a.n_splits = p->num_suffix_splits;
   a.suffix_items = p->batch_size * p->num_kv_heads * p->num_suffix_splits;
   a.final_out = p->num_parts == 1 ? 1 : 0;
+  a.wave_parts = p->suffix_parts_per_item > 1 ? 1 : 0;
   a.parts.o = reinterpret_cast<aios::bf16*>(ws + p->ws_parts_o);
   a.parts.lse = reinterpret_cast<float*>(ws + p->ws_parts_lse);
   a.parts.n_parts = p->num_parts;

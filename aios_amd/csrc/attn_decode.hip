@@ -10,9 +10,11 @@
 //     pages after the prefix.  Its four wavefronts take the item's
 //     32-position sub-tiles round-robin, gather each into their own LDS
 //     region and run the tile engine's math with one 16-row MFMA tile
-//     holding the row's G query heads; the four softmax states are merged
-//     through LDS.  With k_new / v_new given, the row's new token is read
-//     from them and written to its page in the same launch.
+//     holding the row's G query heads.  With the cascade (the combine runs
+//     anyway) every wavefront writes its own partial; otherwise the four
+//     softmax states are merged through LDS.  With k_new / v_new given, the
+//     row's new token is read from them and written to its page in the
+//     same launch.
 // Every workgroup writes a normalised partial (o, lse) into the parts array
 // (layout in kernels.hpp); decode_combine_kernel merges the parts of each
 // (row, kv-head) with m = max lse_j, w_j = 2^(lse_j - m) / sum_i 2^(lse_i - m),
@@ -96,7 +98,8 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
 // wavefronts take the item's 32-position sub-tiles round-robin; each gathers
 // its sub-tile of the row's own pages into its own LDS region (the engine's
 // layout) and runs the engine math with one 16-row MFMA tile whose first G
-// rows are the row's query heads.  The four softmax states are then merged
+// rows are the row's query heads.  Each wavefront then writes its own
+// partial state (DecodeArgs::wave_parts), or the four states are merged
 // through LDS by the first wavefront.
 template <int D, int G>
 __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArgs& a, int item) {
@@ -203,6 +206,52 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
     *reinterpret_cast<uint4*>(const_cast<uint8_t*>(isv ? vc : kc) + new_dst * tok_b + c * 16) = v;
   }
 
+  // Write the G x D rows o / l of one state: staged in LDS (the caller's
+  // free region) in the order of the destination, then full-width 16-byte
+  // stores (one store instruction per 64 chunks instead of one per 16-dim
+  // tile from the G active lanes).  final: bf16 output rows; otherwise part
+  // `part` of the parts array and its lse.
+  auto write_rows = [&](const f32x4 (&acc)[DT], float l_tot, float m, uint8_t* stage_buf,
+                        int part, bool final) {
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    bf16* stage = reinterpret_cast<bf16*>(stage_buf);
+    if (l16 < G) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const f32x4 v = acc[dt] * inv;
+        const int e = final ? l16 * D + dt * 16 + lg * 4 : (dt * G + l16) * 16 + lg * 4;
+        *reinterpret_cast<uint2*>(stage + e) = make_uint2(pack_bf16x2(v[0], v[1]),
+                                                         pack_bf16x2(v[2], v[3]));
+      }
+    }
+    // The same wavefront reads the staged rows back: its LDS accesses
+    // complete in order.
+    constexpr int NCH = G * D / 8;  // 16-byte chunks of the rows
+    for (int c = lane; c < NCH; c += 64) {
+      const uint4 v = reinterpret_cast<const uint4*>(stage)[c];
+      bf16* dst;
+      if (final) {
+        dst = a.out + ((int64_t)b * a.num_qo_heads + h * G) * D + c * 8;
+      } else {
+        const int dt = c * 8 / (G * 16);
+        const int r = c * 8 - dt * G * 16;
+        dst = a.parts.o + a.parts.o_index(D, h, part, b * G + r / 16, dt * 16 + (r & 15));
+      }
+      *reinterpret_cast<uint4*>(dst) = v;
+    }
+    if (!final && lg == 0 && l16 < G)
+      a.parts.lse[a.parts.lse_index(h, part, b * G + l16)] =
+          l_tot > 0.f ? m + fast_log2(l_tot) : kNegInf;
+  };
+
+  if (a.wave_parts) {
+    // One part per wavefront (a wavefront without positions writes an empty
+    // part, l = 0): no merge, no waiting for the slowest wavefront.
+    write_rows(eng.o[0], eng.l_run[0], eng.m_run[0], buf, a.parts.n_chunks + split * NW + wave,
+               false);
+    return;
+  }
+
   // Merge the four wavefronts' states (o relative to each wave's reference
   // m, row totals l) through LDS.
   f32x4* so = reinterpret_cast<f32x4*>(buf);
@@ -245,41 +294,7 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
       acc[dt] += reinterpret_cast<const f32x4*>(lds + w * T::SUB_BYTES)[dt * 64 + lane] * f[w];
   }
 
-  // The G x D result is staged in LDS (wave 0's own region, free now) in
-  // the order of its destination and written with full-width 16-byte
-  // stores: one store instruction per 64 chunks instead of one per 16-dim
-  // tile from the G active lanes (store issue is slow while the CU's memory
-  // pipeline is full of the prefix gathers).
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  bf16* stage = reinterpret_cast<bf16*>(lds);
-  if (l16 < G) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const f32x4 v = acc[dt] * inv;
-      const int e = a.final_out ? l16 * D + dt * 16 + lg * 4 : (dt * G + l16) * 16 + lg * 4;
-      *reinterpret_cast<uint2*>(stage + e) = make_uint2(pack_bf16x2(v[0], v[1]),
-                                                       pack_bf16x2(v[2], v[3]));
-    }
-  }
-  // The same wavefront reads the staged rows back: its LDS accesses
-  // complete in order.
-  constexpr int NCH = G * D / 8;  // 16-byte chunks of the result
-  for (int c = lane; c < NCH; c += 64) {
-    const uint4 v = reinterpret_cast<const uint4*>(stage)[c];
-    bf16* dst;
-    if (a.final_out) {
-      dst = a.out + ((int64_t)b * a.num_qo_heads + h * G) * D + c * 8;
-    } else {
-      const int dt = c * 8 / (G * 16);
-      const int r = c * 8 - dt * G * 16;
-      dst = a.parts.o + a.parts.o_index(D, h, a.parts.n_chunks + split, b * G + r / 16,
-                                        dt * 16 + (r & 15));
-    }
-    *reinterpret_cast<uint4*>(dst) = v;
-  }
-  if (!a.final_out && lg == 0 && l16 < G)
-    a.parts.lse[a.parts.lse_index(h, a.parts.n_chunks + split, b * G + l16)] =
-        l_tot > 0.f ? mx + fast_log2(l_tot) : kNegInf;
+  write_rows(acc, l_tot, mx, lds, a.parts.n_chunks + split, a.final_out != 0);
 }
 
 template <int D, int G>

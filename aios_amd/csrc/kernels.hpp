@@ -55,6 +55,7 @@ struct DecodeArgs {
   int32_t n_splits;
   int32_t suffix_items;  // batch * Hkv * n_splits
   int32_t final_out;     // 1: a single part per (row, head): write bf16 out directly
+  int32_t wave_parts;    // 1: each suffix wavefront writes its own part (no merge)
   PartsArgs parts;
   bf16* out;  // [B][Hq][D]
   // Fused KV append (null k_new: none).  Row b's last KV position is its new
@@ -134,8 +135,9 @@ hipError_t greedy_select(const void* logits, int64_t row_stride, int32_t rows, i
                          int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                          hipStream_t stream);
 
-// KV positions a suffix workgroup gathers per pass (one 32-position engine
-// sub-tile per wavefront).
+// Wavefronts of a suffix workgroup, and the KV positions it gathers per pass
+// (one 32-position engine sub-tile per wavefront).
+constexpr int kSuffixWaves = 4;
 constexpr int kSuffixPass = 128;
 
 // One launch: prefix-chunk workgroups (MFMA tile engine) followed by suffix

@@ -113,7 +113,8 @@ typedef struct aios_attn_plan {
    * issues both.  Lets a profiler bracket the two launches separately. */
   int32_t stage_mask;
   int32_t min_kv_len;        /* shortest row of the batch */
-  int32_t reserved0;
+  int32_t suffix_parts_per_item; /* partial states one suffix item writes: 1 (its
+                                  * wavefronts merge first) or 4 (one per wavefront) */
   /* workspace layout (byte offsets) */
   int64_t ws_parts_o;
   int64_t ws_parts_lse;

@@ -65,7 +65,9 @@ def test_plan_decode_forced_cascade():
     rc, p = _plan(_lib.PHASE_DECODE, np.arange(9), np.cumsum([0] + kv), shared=24, chunk=32)
     assert rc == 0
     assert p.prefix_len == 24 and p.num_prefix_chunks == 1 and p.cascade_rows == 32
-    assert p.num_parts == p.num_prefix_chunks + p.num_suffix_splits
+    # with the cascade every suffix wavefront writes its own part
+    assert p.suffix_parts_per_item == 4
+    assert p.num_parts == p.num_prefix_chunks + 4 * p.num_suffix_splits
     assert p.ws_bytes >= 8 * 2 * p.num_parts * 4 * 96 * 2  # bf16 partial outputs
 
 
@@ -84,6 +86,8 @@ def test_plan_decode_long_rows_without_prefix_split():
     rc, p = _plan(_lib.PHASE_DECODE, np.arange(3), np.cumsum([0, 3000, 17]), shared=0)
     assert rc == 0
     assert p.prefix_len == 0 and p.num_suffix_splits > 1 and p.num_parts <= 64
+    # no cascade: the item's wavefronts merge, one part per item
+    assert p.suffix_parts_per_item == 1 and p.num_parts == p.num_suffix_splits
 
 
 def test_plan_rejects_bad_batches():
