@@ -40,6 +40,8 @@ EXPORTED_SYMBOLS = (
     "aios_linear_rows",
     "aios_linear_rows_ex",
     "aios_greedy_select",
+    "aios_attnres_mix",
+    "aios_attnres_mix_ex",
 )
 
 
@@ -132,6 +134,11 @@ def _declare(lib: ctypes.CDLL) -> None:
                                         _vp, _i64, _vp, _f32, _vp, _i64, _i32, _vp]
     lib.aios_greedy_select.restype = ctypes.c_int
     lib.aios_greedy_select.argtypes = [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]
+    lib.aios_attnres_mix.restype = ctypes.c_int
+    lib.aios_attnres_mix.argtypes = [_vp, _i32, _i64, _i32, _vp, _vp, _f32, _vp, _vp, _vp]
+    lib.aios_attnres_mix_ex.restype = ctypes.c_int
+    lib.aios_attnres_mix_ex.argtypes = [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _f32, _vp, _vp,
+                                        _vp]
 
 
 def lib() -> ctypes.CDLL:

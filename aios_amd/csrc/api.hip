@@ -533,4 +533,55 @@ int aios_greedy_select(const void* logits, int64_t row_stride, int32_t rows, int
                    "greedy_select launch");
 }
 
+static bool overlaps(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes) {
+  if (!a || !b) return false;
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + (uintptr_t)b_bytes && y < x + (uintptr_t)a_bytes;
+}
+
+int aios_attnres_mix_ex(const void* bank, int32_t bank_sources, int64_t num_tokens,
+                        int32_t hidden, const void* partial, const void* delta,
+                        void* partial_out, const float* weighted_query, float eps, float* scores,
+                        void* out, void* stream) {
+  if (bank_sources < 1 || num_tokens < 1 || hidden < 1)
+    return fail(AIOS_ERR_INVALID, "attnres_mix: bank dimensions must be positive");
+  if (num_tokens > 0x7fffffffll)
+    return fail(AIOS_ERR_INVALID, "attnres_mix: num_tokens %lld too large", (long long)num_tokens);
+  const int total = bank_sources + ((partial || delta) ? 1 : 0);
+  if (!aios::attnres_supported(hidden, total))
+    return fail(AIOS_ERR_UNSUPPORTED,
+                "attnres_mix: hidden %d (multiple of 8 up to 8192) or %d sources (<= 64) not built",
+                hidden, total);
+  if (!bank || !weighted_query || !out) return fail(AIOS_ERR_INVALID, "attnres_mix: null pointer");
+  if ((((uintptr_t)bank | (uintptr_t)partial | (uintptr_t)delta | (uintptr_t)partial_out |
+        (uintptr_t)weighted_query | (uintptr_t)out) & 15) != 0)
+    return fail(AIOS_ERR_INVALID, "attnres_mix: tensors must be 16-byte aligned");
+  const int64_t plane = num_tokens * (int64_t)hidden * 2;
+  if (overlaps(out, plane, bank, plane * bank_sources) ||
+      overlaps(partial_out, plane, bank, plane * bank_sources) ||
+      overlaps(out, plane, partial_out, plane) || overlaps(out, plane, partial, plane) ||
+      overlaps(out, plane, delta, plane))
+    return fail(AIOS_ERR_INVALID, "attnres_mix: out / partial_out overlap an input");
+  aios::AttnResArgs a;
+  a.bank = static_cast<const aios::bf16*>(bank);
+  a.bank_sources = bank_sources;
+  a.num_tokens = num_tokens;
+  a.hidden = hidden;
+  a.partial = static_cast<const aios::bf16*>(partial);
+  a.delta = static_cast<const aios::bf16*>(delta);
+  a.partial_out = static_cast<aios::bf16*>(partial_out);
+  a.wq = weighted_query;
+  a.eps = eps;
+  a.scores = scores;
+  a.out = static_cast<aios::bf16*>(out);
+  return check_hip(aios::attnres_mix(a, static_cast<hipStream_t>(stream)), "attnres_mix launch");
+}
+
+int aios_attnres_mix(const void* bank, int32_t bank_sources, int64_t num_tokens, int32_t hidden,
+                     const void* partial, const float* weighted_query, float eps, float* scores,
+                     void* out, void* stream) {
+  return aios_attnres_mix_ex(bank, bank_sources, num_tokens, hidden, partial, nullptr, nullptr,
+                             weighted_query, eps, scores, out, stream);
+}
+
 }  // extern "C"

@@ -135,6 +135,24 @@ hipError_t greedy_select(const void* logits, int64_t row_stride, int32_t rows, i
                          int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                          hipStream_t stream);
 
+// Block-AttnRes depth mix (attnres.hip).  bank [bank_sources][num_tokens]
+// [hidden] and every [num_tokens][hidden] plane contiguous bf16.
+struct AttnResArgs {
+  const bf16* bank;
+  int32_t bank_sources;
+  int64_t num_tokens;
+  int32_t hidden;
+  const bf16* partial;  // may be null
+  const bf16* delta;    // may be null: partial source = bf16(partial + delta)
+  bf16* partial_out;    // receives the formed partial (may be null)
+  const float* wq;      // [hidden] query * key-norm weight
+  float eps;
+  float* scores;  // [total sources][num_tokens] (may be null)
+  bf16* out;
+};
+bool attnres_supported(int hidden, int total_sources);
+hipError_t attnres_mix(const AttnResArgs& a, hipStream_t stream);
+
 // Wavefronts of a suffix workgroup, and the KV positions it gathers per pass
 // (one 32-position engine sub-tile per wavefront).
 constexpr int kSuffixWaves = 4;

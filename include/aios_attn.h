@@ -298,6 +298,40 @@ int aios_greedy_select(const void* logits, int64_t row_stride, int32_t rows, int
                        int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                        void* stream);
 
+/*
+ * Block-AttnRes depth mix.  bank is contiguous bf16 [bank_sources]
+ * [num_tokens][hidden]; partial (may be NULL) a contiguous bf16
+ * [num_tokens][hidden] plane appended as the last source;
+ * weighted_query fp32 [hidden] = query * key_norm.weight.  Per token:
+ *   score_s = <x_s, wq> * rsqrt(mean(x_s^2) + eps)       (fp32)
+ *   w_s     = bf16(softmax over s of score)
+ *   out     = bf16(sum_s w_s * x_s)                      (fp32 sum)
+ * scores (may be NULL) receives score_s at [s * num_tokens + token].
+ * hidden a multiple of 8 up to 8192, at most 64 sources (UNSUPPORTED
+ * otherwise); every pointer 16-byte aligned; out must not overlap an input.
+ * Replaces triton_attnres_mix (python/aios/kernel/attnres.py:130-223; the
+ * mixer of python/aios/models/minimind_ime.py:92-190): one launch that reads
+ * the bank once.
+ */
+int aios_attnres_mix(const void* bank, int32_t bank_sources, int64_t num_tokens, int32_t hidden,
+                     const void* partial, const float* weighted_query, float eps, float* scores,
+                     void* out, void* stream);
+
+/*
+ * aios_attnres_mix with the block's running-partial update folded in: when
+ * delta is not NULL the partial source is bf16(partial + delta) (delta
+ * alone when partial is NULL) -- the `partial + attention_delta` and
+ * `partial + mlp_delta` adds of python/aios/models/minimind_ime.py:233-252 --
+ * and partial_out (if not NULL) receives it.  partial_out may equal partial
+ * (in-place update) or be the bank's next slot bank + bank_sources *
+ * num_tokens * hidden (the block's new depth source, minimind_ime.py:
+ * 305-315); it must not overlap the bank or out.
+ */
+int aios_attnres_mix_ex(const void* bank, int32_t bank_sources, int64_t num_tokens,
+                        int32_t hidden, const void* partial, const void* delta,
+                        void* partial_out, const float* weighted_query, float eps, float* scores,
+                        void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

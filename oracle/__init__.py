@@ -33,6 +33,14 @@ Modules and what pins each function (the checks live in tests/test_oracle.py):
                 Pinned against attention.py.
   prefix.py     token-LCP prefix-reuse plan (ime.py:1116-1168), pinned by the
                 four cases of resources/lesson-14-prefix-kv-reuse/run_lesson14.py.
+  attnres.py    Block-AttnRes depth mixer in float64 (kernel/attnres.py:8-127,
+                models/minimind_ime.py:27-74, 92-190): the expanded (production)
+                form and the materialised form, pinned against each other,
+                against the reference's zero-query known answer
+                (tests/test_ime_attnres.py:59-66), a hand-computed two-source
+                case, closed forms (one source, identical sources, scale
+                invariance of the RMS score), and its bf16 rounding against
+                torch's conversion.
   model.py      float32 CPU restatement of the Qwen3 decoder and the greedy
                 CandidateGroup decode loop (models/qwen3.py:31-173,
                 layers/*.py, ime.py:891-1251) used for full-model Top-1/3

@@ -398,3 +398,91 @@ def test_top3_by_average_distinct_and_ordered():
     ids = torch.tensor([[1, 2], [3, 4], [1, 2], [5, 6], [7, 8]])
     avg = torch.tensor([-1.0, -0.5, -0.2, -3.0, -0.9])
     assert top3_by_average(ids, avg) == [(1, 2), (3, 4), (7, 8)]
+
+
+# --- Block-AttnRes depth mixer ------------------------------------------------
+
+from oracle import attnres as oar  # noqa: E402
+
+
+def test_round_bf16_matches_torch():
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(4096).astype(np.float32) * 10.0,
+                        # exact ties between two bf16 values (round to even)
+                        np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8)],
+                                 dtype=np.float32),
+                        np.array([np.inf, -np.inf, 0.0, -0.0], dtype=np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(oar.round_bf16(x), want)
+
+
+def test_attnres_zero_query_is_uniform_depth_mean():
+    """Known answer of tests/test_ime_attnres.py:59-66: bank = arange(48)
+    as [3, 2, 8], partial = 100, zero query -> mean of the four sources."""
+    bank = np.arange(3 * 2 * 8, dtype=np.float64).reshape(3, 2, 8)
+    partial = np.full((2, 8), 100.0)
+    got = oar.mix(bank, partial, np.zeros(8), np.ones(8), 1e-6)
+    want = (bank.sum(axis=0) + partial) / 4.0
+    assert np.allclose(got, want, rtol=0, atol=1e-12)
+
+
+def test_attnres_expanded_equals_materialized():
+    """tests/test_ime_attnres.py:47-56: the direct (expanded) mixer equals the
+    materialised reference; their query / key-norm weights, seed 7."""
+    g = torch.Generator().manual_seed(7)
+    bank = torch.randn(4, 5, 8, generator=g).double().numpy()
+    partial = torch.randn(5, 8, generator=g).double().numpy()
+    query = np.array([0.3, -0.2, 0.1, 0.4, -0.5, 0.6, 0.2, -0.1])
+    knw = np.array([1.0, 0.9, 1.1, 0.8, 1.2, 1.0, 0.7, 1.3])
+    for p in (None, partial):
+        a = oar.mix(bank, p, query, knw, 1e-6, round_weights=False)
+        b = oar.mix_materialized(bank, p, query, knw, 1e-6, round_weights=False)
+        assert np.allclose(a, b, rtol=1e-12, atol=1e-12)
+    # A dropped key-norm weight or eps, or a sum instead of a mean, changes it.
+    base = oar.mix(bank, partial, query, knw, 1e-6, round_weights=False)
+    assert not np.allclose(base, oar.mix(bank, partial, query, np.ones(8), 1e-6, False))
+    assert not np.allclose(base, oar.mix(bank, partial, query, knw, 1.0, False))
+
+
+def test_attnres_hand_computed_two_sources():
+    """D = 4, x0 = [3, 4, 0, 0], x1 = [0, 0, 1, 1], query e0, key-norm
+    weight [2, 1, 1, 1], eps 0: scores 3*2/2.5 = 2.4 and 0; softmax weights
+    0.9168273 / 0.0831727, bf16 0.91796875 / 0.0830078125."""
+    bank = np.array([[[3.0, 4.0, 0.0, 0.0]], [[0.0, 0.0, 1.0, 1.0]]])
+    q = np.array([1.0, 0.0, 0.0, 0.0])
+    knw = np.array([2.0, 1.0, 1.0, 1.0])
+    sc = oar.scores(bank, None, q, knw, 0.0)
+    assert np.allclose(sc[:, 0], [2.4, 0.0], atol=1e-12)
+    w = oar.softmax_weights(sc)
+    assert w[:, 0].tolist() == [0.91796875, 0.0830078125]
+    got = oar.mix(bank, None, q, knw, 0.0)
+    assert np.allclose(got[0], [2.75390625, 3.671875, 0.0830078125, 0.0830078125], atol=1e-12)
+    # the partial as a last source is the same as a third bank source
+    third = np.array([[0.5, -1.0, 2.0, 0.0]])
+    a = oar.mix(bank, third, q, knw, 1e-6)
+    b = oar.mix(np.concatenate([bank, third[None]]), None, q, knw, 1e-6)
+    assert np.array_equal(a, b)
+
+
+def test_attnres_closed_forms():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((1, 6, 32))
+    q = rng.standard_normal(32)
+    knw = rng.uniform(0.5, 1.5, 32)
+    # one source: weight 1, output = the source
+    assert np.allclose(oar.mix(x, None, q, knw, 1e-6), x[0], atol=0)
+    # identical sources: output = that source (weights sum to 1 before rounding)
+    same = np.repeat(x, 4, axis=0)
+    assert np.allclose(oar.mix(same, None, q, knw, 1e-6, round_weights=False), x[0], atol=1e-12)
+    # RMS normalisation: scaling a source leaves its score unchanged (eps = 0)
+    bank = rng.standard_normal((3, 6, 32))
+    s1 = oar.scores(bank, None, q, knw, 0.0)
+    bank2 = bank.copy()
+    bank2[1] *= 7.5
+    s2 = oar.scores(bank2, None, q, knw, 0.0)
+    assert np.allclose(s1, s2, rtol=1e-12, atol=1e-12)
+    # a dominant score selects its source
+    big = bank.copy()
+    big[2] = np.sign(q * knw)[None, :] * 5.0
+    out = oar.mix(big, None, q * 100.0, knw, 1e-6, round_weights=False)
+    assert np.allclose(out, big[2], atol=1e-6)
