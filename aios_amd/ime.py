@@ -33,7 +33,7 @@ from aios_amd.config import ModelConfig
 from aios_amd.core import Batch, Context, Req, SamplingParams, reset_global_ctx, set_global_ctx
 from aios_amd.kvcache import MHAKVCache
 from aios_amd.paged import greedy_select
-from aios_amd.qwen3 import Qwen3ForCausalLM
+from aios_amd.minimind_ime import build_causal_lm
 from aios_amd.scheduler import CacheManager
 
 
@@ -125,7 +125,7 @@ class CandidateGroupRuntime:
         self.num_pages = num_pages
         self.max_attempts = max_attempts
         backend = Mi355xAttentionBackend(config, workspace_size=workspace_size)
-        self.model = Qwen3ForCausalLM(config, weights, self.device, attn_backend=backend)
+        self.model = build_causal_lm(config, weights, self.device, attn_backend=backend)
         self.kv_cache = MHAKVCache(config.num_kv_heads, config.num_layers, config.head_dim,
                                    num_pages, 1, torch.bfloat16, self.device)
         self.cache_manager = CacheManager(self.device, num_pages)

@@ -1,7 +1,8 @@
 """Decoder-layer ops on the gfx950 kernels (the layers the reference takes
-from FlashInfer and torch: python/aios/layers/norm.py:10-40,
-layers/activation.py:9-12, layers/attention.py:11-16 and the q/k norm of
-models/qwen3.py:65-66).
+from FlashInfer, Triton and torch: python/aios/layers/norm.py:10-40,
+layers/activation.py:9-12, layers/attention.py:11-16, the q/k norm of
+models/qwen3.py:65-66 and the Block-AttnRes depth mixer,
+kernel/attnres.py:130-223).
 
 ``HipOps`` is the op set the decoder uses on the GPU; every call goes
 through the C ABI of libaios_attn.so and fails loudly without it.
@@ -125,6 +126,23 @@ class HipOps:
             positions.contiguous().data_ptr(), q.data_ptr(), k.data_ptr(), eps, _stream(qkv)),
             "aios_qk_norm_rope")
         return q, k
+
+    @staticmethod
+    def attnres_mix(bank: torch.Tensor, partial: torch.Tensor | None,
+                    weighted_query: torch.Tensor, eps: float) -> torch.Tensor:
+        """Depth mix of bank [S, N, D] (+ partial as the last source)."""
+        from aios_amd.kernel import attnres_mix
+
+        return attnres_mix(bank, partial, weighted_query, eps)
+
+    @staticmethod
+    def attnres_mix_step(bank: torch.Tensor, partial: torch.Tensor | None, delta: torch.Tensor,
+                         weighted_query: torch.Tensor, eps: float,
+                         partial_out: torch.Tensor) -> torch.Tensor:
+        """partial_out <- partial + delta, then the mix with it as the last source."""
+        from aios_amd.kernel import attnres_mix_step
+
+        return attnres_mix_step(bank, partial, delta, weighted_query, eps, partial_out)
 
     @staticmethod
     def silu_and_mul(x: torch.Tensor) -> torch.Tensor:

@@ -48,6 +48,18 @@ def init_weights(config: ModelConfig, seed: int, device="cpu",
             "gate_up": lin(2 * config.intermediate_size, h),
             "down": lin(h, config.intermediate_size),
         })
+        if config.residual_type == "block_attnres":
+            # the two depth mixers of the layer (minimind_ime.py:208-213):
+            # routing query and key-norm weight each
+            w["layers"][-1].update({
+                "attn_res_query": lin(1, h)[0],
+                "attn_res_norm": torch.ones(h, device=dev, dtype=dtype),
+                "mlp_res_query": lin(1, h)[0],
+                "mlp_res_norm": torch.ones(h, device=dev, dtype=dtype),
+            })
+    if config.residual_type == "block_attnres":
+        w["final_res_query"] = lin(1, h)[0]
+        w["final_res_norm"] = torch.ones(h, device=dev, dtype=dtype)
     return w
 
 
@@ -55,8 +67,9 @@ def weights_to(w: dict, device, dtype=None) -> dict:
     def mv(t):
         t = t.to(device)
         return t.to(dtype) if dtype is not None else t
-    return {"embed": mv(w["embed"]), "final_norm": mv(w["final_norm"]),
-            "layers": [{k: mv(v) for k, v in lw.items()} for lw in w["layers"]]}
+    out = {k: mv(v) for k, v in w.items() if k != "layers"}
+    out["layers"] = [{k: mv(v) for k, v in lw.items()} for lw in w["layers"]]
+    return out
 
 
 class RotaryEmbedding:

@@ -10,6 +10,10 @@ for a token sequence:
   RMSNorm (layers/norm.py:18-40), SwiGLU MLP (layers/activation.py:9-12);
 * model (qwen3.py:112-173): embedding, layers, final norm, tied LM head
   (layers/embedding.py:13-41);
+* the Block-AttnRes trunk of the 0.214B MiniMind-IME model
+  (minimind_ime.py:193-326) with its depth mixers in the materialised
+  form (:125-150): a list of bank sources, the block's running partial,
+  a mixer before every attention and MLP and a final mixer;
 * candidate rule of the CandidateGroup engine (ime.py:891-1115 with greedy
   sampling): candidate i starts from the i-th most likely first token, then
   takes the argmax at every step; the score is the average raw log-prob.
@@ -25,8 +29,9 @@ import torch
 
 def _w32(w: dict) -> dict:
     f = lambda t: t.detach().to("cpu", torch.float32)
-    return {"embed": f(w["embed"]), "final_norm": f(w["final_norm"]),
-            "layers": [{k: f(v) for k, v in lw.items()} for lw in w["layers"]]}
+    out = {k: f(v) for k, v in w.items() if k != "layers"}
+    out["layers"] = [{k: f(v) for k, v in lw.items()} for lw in w["layers"]]
+    return out
 
 
 def _rms(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
@@ -49,16 +54,50 @@ class OracleModel:
         self.c = config
         self.w = _w32(weights)
 
+    def _attention(self, lw: dict, x: torch.Tensor) -> torch.Tensor:
+        """Self-attention of normalised hidden states x [B, L, H] at positions
+        0..L-1 (qwen3.py:52-75): projection, q/k norm, RoPE, causal GQA, o_proj."""
+        c = self.c
+        b, n, _ = x.shape
+        hq, hkv, d = c.num_qo_heads, c.num_kv_heads, c.head_dim
+        g = hq // hkv
+        pos = torch.arange(n)
+        mask = torch.ones(n, n, dtype=torch.bool).tril()
+        qkv = x @ lw["qkv"].T
+        q, k, v = qkv.split([hq * d, hkv * d, hkv * d], dim=-1)
+        q = _rms(q.reshape(b, n, hq, d), lw["q_norm"], c.rms_norm_eps)
+        k = _rms(k.reshape(b, n, hkv, d), lw["k_norm"], c.rms_norm_eps)
+        v = v.reshape(b, n, hkv, d)
+        q = _rope(q, pos, c.rope_theta)
+        k = _rope(k, pos, c.rope_theta)
+        k = k.repeat_interleave(g, dim=2)
+        v = v.repeat_interleave(g, dim=2)
+        s = torch.einsum("bihd,bjhd->bhij", q, k) * d ** -0.5
+        s = s.masked_fill(~mask, float("-inf"))
+        o = torch.einsum("bhij,bjhd->bihd", s.softmax(-1), v).reshape(b, n, hq * d)
+        return o @ lw["o"].T
+
+    @staticmethod
+    def _mlp(lw: dict, x: torch.Tensor) -> torch.Tensor:
+        gate, up = (x @ lw["gate_up"].T).chunk(2, dim=-1)
+        return (torch.nn.functional.silu(gate) * up) @ lw["down"].T
+
+    def _mix(self, sources: list, query: torch.Tensor, key_norm: torch.Tensor) -> torch.Tensor:
+        """Depth mixer in its materialised form (minimind_ime.py:125-150):
+        normalise each source, dot with the query, softmax over depth."""
+        x = torch.stack(sources, 0)
+        normalized = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.c.rms_norm_eps)
+        logits = (normalized * key_norm * query).sum(-1)
+        w = logits.softmax(0)
+        return (w[..., None] * x).sum(0)
+
     @torch.no_grad()
     def logits(self, ids: torch.Tensor, start: int = 0) -> torch.Tensor:
         """ids [B, L] int64 -> logits [B, L - start, V] float32 of positions
         start..L-1 (causal attention, positions 0..L-1)."""
         c = self.c
-        b, n = ids.shape
-        hq, hkv, d = c.num_qo_heads, c.num_kv_heads, c.head_dim
-        g = hq // hkv
-        pos = torch.arange(n)
-        mask = torch.ones(n, n, dtype=torch.bool).tril()
+        if c.residual_type == "block_attnres":
+            return self._attnres_logits(ids, start)
         h = self.w["embed"][ids]
         residual = None
         for lw in self.w["layers"]:
@@ -66,25 +105,34 @@ class OracleModel:
                 residual = h
             else:
                 residual = h + residual
-            x = _rms(residual, lw["input_norm"], c.rms_norm_eps)
-            qkv = x @ lw["qkv"].T
-            q, k, v = qkv.split([hq * d, hkv * d, hkv * d], dim=-1)
-            q = _rms(q.reshape(b, n, hq, d), lw["q_norm"], c.rms_norm_eps)
-            k = _rms(k.reshape(b, n, hkv, d), lw["k_norm"], c.rms_norm_eps)
-            v = v.reshape(b, n, hkv, d)
-            q = _rope(q, pos, c.rope_theta)
-            k = _rope(k, pos, c.rope_theta)
-            k = k.repeat_interleave(g, dim=2)
-            v = v.repeat_interleave(g, dim=2)
-            s = torch.einsum("bihd,bjhd->bhij", q, k) * d ** -0.5
-            s = s.masked_fill(~mask, float("-inf"))
-            o = torch.einsum("bhij,bjhd->bihd", s.softmax(-1), v).reshape(b, n, hq * d)
-            x = o @ lw["o"].T
+            x = self._attention(lw, _rms(residual, lw["input_norm"], c.rms_norm_eps))
             residual = x + residual
-            x = _rms(residual, lw["post_norm"], c.rms_norm_eps)
-            gate, up = (x @ lw["gate_up"].T).chunk(2, dim=-1)
-            h = (torch.nn.functional.silu(gate) * up) @ lw["down"].T
+            h = self._mlp(lw, _rms(residual, lw["post_norm"], c.rms_norm_eps))
         x = _rms(h + residual, self.w["final_norm"], c.rms_norm_eps)
+        return x[:, start:] @ self.w["embed"].T
+
+    def _attnres_logits(self, ids: torch.Tensor, start: int) -> torch.Tensor:
+        """Block-AttnRes trunk (minimind_ime.py:193-326): a bank of the
+        embedding and one summed delta per finished block; every layer mixes
+        the bank (plus the block's running partial) before its attention and
+        before its MLP; a final mixer over the whole bank feeds the norm."""
+        c = self.c
+        per = c.num_layers // c.attnres_num_blocks
+        bank = [self.w["embed"][ids]]
+        partial = None
+        for i, lw in enumerate(self.w["layers"]):
+            if i % per == 0:
+                partial = None
+            srcs = bank if partial is None else bank + [partial]
+            h = self._mix(srcs, lw["attn_res_query"], lw["attn_res_norm"])
+            delta = self._attention(lw, _rms(h, lw["input_norm"], c.rms_norm_eps))
+            partial = delta if partial is None else partial + delta
+            h = self._mix(bank + [partial], lw["mlp_res_query"], lw["mlp_res_norm"])
+            partial = partial + self._mlp(lw, _rms(h, lw["post_norm"], c.rms_norm_eps))
+            if (i + 1) % per == 0:
+                bank.append(partial)
+        h = self._mix(bank, self.w["final_res_query"], self.w["final_res_norm"])
+        x = _rms(h, self.w["final_norm"], c.rms_norm_eps)
         return x[:, start:] @ self.w["embed"].T
 
     @torch.no_grad()

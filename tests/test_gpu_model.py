@@ -20,7 +20,7 @@ from dataclasses import replace
 import pytest
 import torch
 
-from aios_amd.config import MINIMIND_0P1B, MINIMIND_IME_0P1B, QWEN3_0P6B
+from aios_amd.config import MINIMIND_0P1B, MINIMIND_ATTNRES_0P214B, MINIMIND_IME_0P1B, QWEN3_0P6B
 from aios_amd.core import reset_global_ctx
 from aios_amd.ime import CancellationToken, CandidateGroupConfig, CandidateGroupEngine, CandidateGroupRuntime
 from aios_amd.qwen3 import init_weights, weights_to
@@ -318,3 +318,51 @@ def test_graph_replay_eos_masks_rows():
         assert gap[1:].max().item() <= 2 * LOGIT_TOL_TIGHT
     assert eng.rt.cache_manager.available_size == eng.rt.num_pages - 32
 
+
+
+# --- Block-AttnRes (0.214B-shaped) trunk -----------------------------------------
+
+def test_prefix_logits_attnres_0p214b():
+    """64-token prefix through the 32-layer, 8-block depth-routed trunk (65
+    mixers) vs the float32 oracle trunk."""
+    c = MINIMIND_ATTNRES_0P214B
+    eng, om = _engine(c, 3)
+    prefix = _prefix(3, 64, c.vocab_size)
+    res = eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=1))
+    gpu = res.prefix_logits[0].float().cpu()
+    ref = om.logits(torch.tensor(prefix)[None], 63)[0, -1]
+    assert (gpu - ref).abs().max().item() <= LOGIT_TOL_TIGHT
+    assert torch.nn.functional.cosine_similarity(gpu, ref, dim=0).item() > 0.999
+    for k in (1, 3):
+        assert _set_equal_if_screened(gpu, ref, k) in (True, None)
+
+
+def test_candidate_group_attnres_0p214b():
+    """8 candidates x 12 greedy steps on the Block-AttnRes trunk: every
+    decode step's logits against the oracle on the GPU's own histories."""
+    c = MINIMIND_ATTNRES_0P214B
+    eng, om = _engine(c, 20260814)
+    _check_candidate_group(eng, om, _prefix(20260814, 64, c.vocab_size), 8, 12)
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages - 64
+
+
+def test_graph_replay_matches_eager_attnres():
+    c = MINIMIND_ATTNRES_0P214B.with_layers(8)
+    w = init_weights(c, 5, "cpu")
+    rt = CandidateGroupRuntime(c, weights_to(w, "cuda"), "cuda", num_pages=1024)
+    eager = CandidateGroupEngine(rt, use_graphs=False)
+    graphed = CandidateGroupEngine(rt, use_graphs=True)
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=10)
+    om = OracleModel(c, w)
+    for seed in (5, 6, 5):
+        prefix = _prefix(seed, 64, c.vocab_size)
+        e = eager.complete(prefix, cfg)
+        eager.reset_prefix_cache()
+        torch.cuda.synchronize()
+        g = graphed.complete(prefix, cfg)
+        graphed.reset_prefix_cache()
+        assert [x.token_ids for x in g.raw_candidates] == [x.token_ids for x in e.raw_candidates]
+        assert [x.average_logprob for x in g.raw_candidates] == \
+            [x.average_logprob for x in e.raw_candidates]
+        _check_against_oracle(g, om, prefix, 8, 10)
+    assert rt.cache_manager.available_size == rt.num_pages

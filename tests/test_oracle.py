@@ -486,3 +486,83 @@ def test_attnres_closed_forms():
     big[2] = np.sign(q * knw)[None, :] * 5.0
     out = oar.mix(big, None, q * 100.0, knw, 1e-6, round_weights=False)
     assert np.allclose(out, big[2], atol=1e-6)
+
+
+def _tiny_attnres(**kw):
+    base = dict(num_layers=8, residual_type="block_attnres", attnres_num_blocks=2)
+    base.update(kw)
+    return _tiny_config(**base)
+
+
+def test_attnres_config_gates():
+    """tests/test_ime_attnres.py:81-85: partial migration and a bad layer
+    partition are rejected."""
+    with pytest.raises(ValueError, match="alpha=1.0"):
+        _tiny_attnres(attnres_alpha=0.5)
+    with pytest.raises(ValueError, match="divisible"):
+        _tiny_attnres(num_layers=7)
+    assert _tiny_attnres().layers_per_attnres_block == 4
+
+
+def test_oracle_attnres_zero_blocks_is_normalised_embedding():
+    """Zero projections and zero routing queries: every delta is zero, every
+    mixer averages its sources, the final mixer returns embed / 3 (bank of
+    the embedding and two zero blocks) and the final RMSNorm removes the
+    scale: logits = RMSNorm(embed[ids]) @ embed^T."""
+    from aios_amd.qwen3 import init_weights
+
+    c = _tiny_attnres(rms_norm_eps=1e-12)
+    w = init_weights(c, 0, "cpu", dtype=torch.float32, std=0.1)
+    for lw in w["layers"]:
+        for key in ("qkv", "o", "gate_up", "down", "attn_res_query", "mlp_res_query"):
+            lw[key].zero_()
+    w["final_res_query"].zero_()
+    ids = torch.tensor([[3, 7, 7, 1]])
+    e = w["embed"][ids]
+    ref = (e * torch.rsqrt(e.pow(2).mean(-1, keepdim=True))) @ w["embed"].T
+    assert torch.allclose(OracleModel(c, w).logits(ids), ref, atol=1e-5)
+
+
+def test_oracle_attnres_model_matches_product_composition():
+    """The oracle's list-of-sources trunk with materialised mixers and the
+    product's fused form (expanded mixers, partial formed inside the next
+    mixer, block sums written into the bank's next slot) agree in float32."""
+    from aios_amd.core import Batch, Context, Req, SamplingParams, reset_global_ctx, set_global_ctx
+    from aios_amd.minimind_ime import MiniMindBlockAttnResForCausalLM
+    from aios_amd.qwen3 import init_weights
+    from tests.util import TorchOps
+
+    c = _tiny_attnres()
+    w = init_weights(c, 2, "cpu", dtype=torch.float32, std=0.2)
+    for lw in w["layers"]:
+        for key in ("input_norm", "post_norm", "q_norm", "k_norm", "attn_res_norm",
+                    "mlp_res_norm"):
+            lw[key].uniform_(0.5, 1.5)
+        lw["attn_res_query"].mul_(20.0)  # routing far from uniform
+        lw["mlp_res_query"].mul_(20.0)
+    w["final_res_query"].mul_(20.0)
+    ids = torch.tensor([5, 9, 2, 44, 0, 13, 8])
+    backend = _DenseCpuBackend(c.head_dim ** -0.5)
+    model = MiniMindBlockAttnResForCausalLM(c, w, "cpu", attn_backend=backend, max_positions=64,
+                                            ops=TorchOps())
+    reset_global_ctx()
+    ctx = Context(page_size=1)
+    ctx.kv_cache = None
+    set_global_ctx(ctx)
+    try:
+        req = Req(input_ids=ids, cached_len=0, output_len=1, uid=0,
+                  sampling_params=SamplingParams(), table_idx=0)
+        batch = Batch(reqs=[req], phase="prefill", return_all_logits=True)
+        batch.input_ids = ids
+        batch.positions = torch.arange(len(ids), dtype=torch.int32)
+        backend.prepare_metadata(batch)
+        with ctx.forward_batch(batch):
+            got = model.forward()
+    finally:
+        reset_global_ctx()
+    om = OracleModel(c, w)
+    ref = om.logits(ids[None])[0]
+    assert torch.allclose(got, ref, atol=1e-4, rtol=1e-4)
+    # the mixers matter: the standard trunk on the same weights differs
+    std = OracleModel(_tiny_config(num_layers=8), w).logits(ids[None])[0]
+    assert not torch.allclose(std, ref, atol=1e-2)

@@ -55,6 +55,19 @@ class TorchOps:
 
         return q * c + rot(q) * s, k * c + rot(k) * s
 
+    def attnres_mix(self, bank, partial, weighted_query, eps):
+        """kernel/attnres.py:8-127: fp32 RMS scores, fp32 softmax, weights
+        rounded to the bank dtype, fp32 weighted sum."""
+        src = bank if partial is None else torch.cat((bank, partial[None]), 0)
+        x = src.float()
+        sc = (x * weighted_query.float()).sum(-1) * torch.rsqrt(x.pow(2).mean(-1) + eps)
+        w = sc.softmax(0).to(bank.dtype).float()
+        return (w[:, :, None] * x).sum(0).to(bank.dtype)
+
+    def attnres_mix_step(self, bank, partial, delta, weighted_query, eps, partial_out):
+        partial_out.copy_(delta if partial is None else partial + delta)
+        return self.attnres_mix(bank, partial_out, weighted_query, eps)
+
     def silu_and_mul(self, x):
         g, u = x.chunk(2, dim=-1)
         return torch.nn.functional.silu(g) * u
