@@ -31,6 +31,50 @@ from aios_amd.core import get_global_ctx
 from aios_amd.qwen3 import Qwen3ForCausalLM
 
 
+class DepthBank:
+    """The depth bank of one forward and the block's running partial, with
+    the mixer calls that advance them (minimind_ime.py:215-252, 287-326).
+
+    ``add(delta, closes_block)`` records a layer's delta without touching
+    memory; the next ``mix`` forms ``partial + delta`` inside its launch and
+    stores it -- into the partial buffer, or, when the delta closed a block,
+    into the bank's next slot (the block's new depth source).
+    """
+
+    def __init__(self, storage: torch.Tensor, part_buf: torch.Tensor, ops, eps: float) -> None:
+        self.storage = storage      # [blocks + 1, tokens, hidden]; storage[0] = embedding
+        self.part_buf = part_buf    # [tokens, hidden]
+        self.ops = ops
+        self.eps = eps
+        self.count = 1              # sources in the bank
+        self.partial = None         # the block's running partial, as materialised so far
+        self.pending = None         # the delta not yet added into it
+        self.to_bank = False        # pending closes its block
+
+    def add(self, delta: torch.Tensor, closes_block: bool = False) -> None:
+        if self.pending is not None:
+            raise RuntimeError("two deltas without a mix between them")
+        self.pending = delta
+        self.to_bank = closes_block
+
+    def mix(self, weighted_query: torch.Tensor) -> torch.Tensor:
+        bank = self.storage[: self.count]
+        if self.pending is None:
+            return self.ops.attnres_mix(bank, self.partial, weighted_query, self.eps)
+        if self.to_bank:
+            out = self.ops.attnres_mix_step(bank, self.partial, self.pending, weighted_query,
+                                            self.eps, self.storage[self.count])
+            self.count += 1
+            self.partial = None
+        else:
+            out = self.ops.attnres_mix_step(bank, self.partial, self.pending, weighted_query,
+                                            self.eps, self.part_buf)
+            self.partial = self.part_buf
+        self.pending = None
+        self.to_bank = False
+        return out
+
+
 class MiniMindBlockAttnResForCausalLM(Qwen3ForCausalLM):
     """Block-AttnRes decoder + tied LM head (minimind_ime.py:255-354).
     Mixer weights per layer: ``attn_res_query`` / ``attn_res_norm`` and
@@ -68,41 +112,18 @@ class MiniMindBlockAttnResForCausalLM(Qwen3ForCausalLM):
                            device=embed.device)
         torch.index_select(embed, 0, ids, out=bank[0])
         part_buf = torch.empty((t, c.hidden_size), dtype=embed.dtype, device=embed.device)
-
-        count = 1          # sources in the bank
-        partial = None     # the block's running partial, as materialised so far
-        pending = None     # the delta not yet added into it
-        to_bank = False    # pending closes its block: the sum becomes bank[count]
-
-        def mix(weighted_query):
-            nonlocal count, partial, pending, to_bank
-            if pending is None:
-                return ops.attnres_mix(bank[:count], partial, weighted_query, eps)
-            if to_bank:
-                out = ops.attnres_mix_step(bank[:count], partial, pending, weighted_query, eps,
-                                           bank[count])
-                count += 1
-                partial = None
-            else:
-                out = ops.attnres_mix_step(bank[:count], partial, pending, weighted_query, eps,
-                                           part_buf)
-                partial = part_buf
-            pending = None
-            to_bank = False
-            return out
-
+        depth = DepthBank(bank, part_buf, ops, eps)
         positions = batch.positions
         for i, lw in enumerate(self.w["layers"]):
-            h = mix(self._wq_attn[i])
+            h = depth.mix(self._wq_attn[i])
             qkv, _ = ops.add_rmsnorm_linear(h, None, lw["input_norm"], eps, lw["qkv"])
-            pending = self._attention(i, qkv, positions, ctx.kv_cache, batch)
-            h = mix(self._wq_mlp[i])
+            depth.add(self._attention(i, qkv, positions, ctx.kv_cache, batch))
+            h = depth.mix(self._wq_mlp[i])
             act, _ = ops.add_rmsnorm_linear(h, None, lw["post_norm"], eps, lw["gate_up"],
                                             silu=True)
-            pending = ops.linear(act, lw["down"])
-            to_bank = (i + 1) % per_block == 0
-        h = mix(self._wq_final)
-        if count != c.attnres_num_blocks + 1:
+            depth.add(ops.linear(act, lw["down"]), closes_block=(i + 1) % per_block == 0)
+        h = depth.mix(self._wq_final)
+        if depth.count != c.attnres_num_blocks + 1:
             raise RuntimeError("AttnRes block produced no residual delta")
         if batch.is_prefill and not batch.return_all_logits:
             h = h[batch.attn_metadata.get_last_indices(batch.size)]

@@ -17,7 +17,10 @@ full-model CandidateGroup Top-3 latency of the MiniMind-0.1B-shaped model
 (``candidate_group``: p50/p95 over 30 seeded prefixes after 5 warmups, with
 graph-replayed and eager decode steps) and of the Qwen3-0.6B-shaped model
 on a 128-token prefix extended by 2 ids (``candidate_group_qwen3_0p6b``:
-the cross-keystroke case, 8 candidates x 24 steps), the reference's CPU attention
+the cross-keystroke case, 8 candidates x 24 steps) and of the 0.214B
+Block-AttnRes-shaped model (``candidate_group_attnres_0p214b``: 64-token
+prefix, 8 candidates x 32 steps, 65 depth mixers per forward), the 65-mixer
+depth-routing pipeline alone (``attnres_pipeline``), the reference's CPU attention
 path (restated, oracle/sdpa_cpu.py) timed on a bounded sample on the host
 cores, and the causal prefill of the 4096-token prefix (``prefill``: one
 layer, TFLOP/s against the MFMA bf16 peak).  ``roofline.traffic`` is the HBM
@@ -232,6 +235,109 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int 
     return out
 
 
+def attnres_pipeline(seed: int, warmups: int = 5, iters: int = 50) -> dict:
+    """The 65 depth mixers of one forward of the 0.214B Block-AttnRes trunk
+    (32 layers in 8 blocks of 4: a mixer before each attention and each MLP,
+    one final mixer) at N = 8 rows, hidden 768 -- the reference's mixer
+    pipeline microbenchmark shape (N=8, D=768, 65 mixers, 5 warmups, 50
+    timed).  Each mixer is one launch of the depth-mix kernel, which also
+    forms the block's running partial from the previous delta and stores
+    each block's sum into the bank; the deltas are fixed synthetic tensors
+    (the attention/MLP work between mixers is not part of this leg).  Timed
+    eagerly (65 launches from Python per pipeline) and as one captured graph.
+    """
+    import statistics
+
+    import torch
+
+    from aios_amd.layers import HipOps
+    from aios_amd.minimind_ime import DepthBank
+
+    dev = torch.device("cuda:0")
+    n, d, layers, per, eps = 8, 768, 32, 4, 1e-5
+    g = torch.Generator(device=dev).manual_seed(seed)
+    storage = torch.empty((layers // per + 1, n, d), device=dev, dtype=torch.bfloat16)
+    storage[0] = (torch.randn(n, d, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    part = torch.empty((n, d), device=dev, dtype=torch.bfloat16)
+    deltas = (torch.randn(2 * layers, n, d, generator=g, device=dev) * 0.3).to(torch.bfloat16)
+    wqs = torch.randn(2 * layers + 1, d, generator=g, device=dev) * 0.05
+    ops = HipOps()
+
+    # algorithmic bytes: every source read once, the formed partial's inputs
+    # read and its result written, the output written, the query read
+    plane = n * d * 2
+    total_bytes, count, has_partial, pending = 0, 1, False, False
+    for m in range(2 * layers + 1):
+        total_bytes += count * plane + plane + d * 4
+        if pending:
+            total_bytes += (2 if has_partial else 1) * plane + plane
+            closes = m % 2 == 0 and m > 0 and (m // 2) % per == 0
+            if closes:
+                count, has_partial = count + 1, False
+            else:
+                has_partial = True
+        elif has_partial:
+            total_bytes += plane
+        pending = m < 2 * layers
+
+    def run():
+        bank = DepthBank(storage, part, ops, eps)
+        for i in range(layers):
+            bank.mix(wqs[2 * i])
+            bank.add(deltas[2 * i])
+            bank.mix(wqs[2 * i + 1])
+            bank.add(deltas[2 * i + 1], closes_block=(i + 1) % per == 0)
+        out = bank.mix(wqs[-1])
+        assert bank.count == layers // per + 1
+        return out
+
+    eager_ms = []
+    for i in range(warmups + iters):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ref = run()
+        torch.cuda.synchronize()
+        if i >= warmups:
+            eager_ms.append((time.perf_counter() - t0) * 1e3)
+    ref = ref.clone()
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        run()
+        with torch.cuda.graph(graph, stream=s):
+            out = run()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    graph_ms = []
+    for i in range(warmups + iters):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        graph.replay()
+        torch.cuda.synchronize()
+        if i >= warmups:
+            graph_ms.append((time.perf_counter() - t0) * 1e3)
+    matches = bool(torch.equal(out, ref))
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    gpu_ms = e0.elapsed_time(e1) / iters
+    mixers = 2 * layers + 1
+    gbps = total_bytes / (gpu_ms * 1e-3) / 1e9
+    return {"workload": "65 depth mixers of the 0.214B Block-AttnRes trunk (32 layers, 8 blocks), "
+                        "N=8 rows, hidden 768, bf16",
+            "mixers": mixers, "eager_pipeline_ms_p50": round(statistics.median(eager_ms), 4),
+            "graph_pipeline_ms_p50": round(statistics.median(graph_ms), 4),
+            "graph_gpu_ms": round(gpu_ms, 4),
+            "us_per_mixer_graph": round(gpu_ms * 1e3 / mixers, 3),
+            "algorithmic_bytes_per_pipeline": total_bytes, "achieved_gbps": round(gbps, 1),
+            "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4), "bound": "launch latency",
+            "graph_matches_eager": matches}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -419,6 +525,8 @@ def main() -> int:
     del wl, out, ws, ws2, k_new, v_new, main_calls, comb_calls, graph
     torch.cuda.empty_cache()
     _log(f"decode step {ms_per_step * 1e3:.1f} us; main kernel {casc_ms * 1e3:.2f} us")
+    result["attnres_pipeline"] = attnres_pipeline(args.seed)
+    _log(f"attnres pipeline {result['attnres_pipeline']['graph_pipeline_ms_p50']} ms (graph)")
     result["prefill"] = prefix_prefill(args.seed)
     _log(f"prefix prefill {result['prefill']['avg_launch_us']} us")
     if not args.no_candidate_group:
@@ -431,6 +539,11 @@ def main() -> int:
             warmups=3)
         _log(f"candidate group qwen3-0.6b "
              f"{result['candidate_group_qwen3_0p6b']['graph']['top3_p50_ms']} ms p50")
+        result["candidate_group_attnres_0p214b"] = candidate_group(
+            args.seed, model="minimind-attnres-0.214b", prefix_tokens=64, steps=32, runs=20,
+            warmups=3)
+        _log(f"candidate group attnres-0.214b "
+             f"{result['candidate_group_attnres_0p214b']['graph']['top3_p50_ms']} ms p50")
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cpu_wl, args.cpu_seconds)
         _log("cpu baseline done")

@@ -54,7 +54,9 @@ CASES = [
     (5, 8, 768, True),     # tests/test_ime_attnres.py:88-108 shape
     (9, 8, 768, False),    # the final mixer of the 8-block trunk
     (8, 64, 768, True),    # prefill of a 64-token prefix
-    (3, 7, 1024, True),
+    (3, 7, 1024, True),    # the one-wavefront-per-token kernel: hidden 256..1024
+    (6, 9, 256, True),
+    (12, 4, 1280, True),   # the workgroup kernel, all sources in registers
     (16, 5, 256, True),    # 17 sources: the re-reading path
     (40, 3, 8192, True),   # widest hidden, 41 sources
     (2, 1, 8, False),      # smallest hidden
@@ -87,8 +89,9 @@ def test_attnres_zero_query_is_uniform_mean():
     assert torch.equal(out.float(), want.to(torch.bfloat16).float())
 
 
-def test_attnres_step_fuses_partial_update():
-    s, n, d = 4, 8, 768
+@pytest.mark.parametrize("s,d", [(4, 768), (4, 1280), (20, 512)])
+def test_attnres_step_fuses_partial_update(s, d):
+    n = 8
     bank, partial, query, knw, wq = _inputs(s, n, d, True, 7)
     delta = _bf16((n, d), 9, 0.7)
     p_out = torch.empty_like(partial)
