@@ -42,6 +42,8 @@ EXPORTED_SYMBOLS = (
     "aios_greedy_select",
     "aios_attnres_mix",
     "aios_attnres_mix_ex",
+    "aios_stateless_uniforms",
+    "aios_sample",
 )
 
 
@@ -134,6 +136,11 @@ def _declare(lib: ctypes.CDLL) -> None:
                                         _vp, _i64, _vp, _f32, _vp, _i64, _i32, _vp]
     lib.aios_greedy_select.restype = ctypes.c_int
     lib.aios_greedy_select.argtypes = [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]
+    lib.aios_stateless_uniforms.restype = ctypes.c_int
+    lib.aios_stateless_uniforms.argtypes = [_vp, _i32, _i32, _vp, _vp]
+    lib.aios_sample.restype = ctypes.c_int
+    lib.aios_sample.argtypes = [_vp, _i64, _i32, _i32, _i32, _f32, _i32, _f32, _vp, _i64, _i32,
+                                _vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp]
     lib.aios_attnres_mix.restype = ctypes.c_int
     lib.aios_attnres_mix.argtypes = [_vp, _i32, _i64, _i32, _vp, _vp, _f32, _vp, _vp, _vp]
     lib.aios_attnres_mix_ex.restype = ctypes.c_int

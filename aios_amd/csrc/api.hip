@@ -533,6 +533,76 @@ int aios_greedy_select(const void* logits, int64_t row_stride, int32_t rows, int
                    "greedy_select launch");
 }
 
+int aios_stateless_uniforms(const int64_t* seeds, int32_t rows, int32_t steps, float* out,
+                            void* stream) {
+  if (rows < 0 || steps < 1)
+    return fail(AIOS_ERR_INVALID, "stateless_uniforms: steps must be positive (rows=%d steps=%d)",
+                rows, steps);
+  if (rows == 0) return AIOS_OK;
+  if (!seeds || !out) return fail(AIOS_ERR_INVALID, "stateless_uniforms: null pointer");
+  return check_hip(aios::stateless_uniforms(seeds, rows, steps, out,
+                                            static_cast<hipStream_t>(stream)),
+                   "stateless_uniforms launch");
+}
+
+int aios_sample(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                int32_t elem_bytes, float temperature, int32_t top_k, float top_p,
+                const float* uniforms, int64_t uniform_stride, int32_t uniform_count,
+                const int64_t* step, const int32_t* forbidden, int32_t n_forbidden,
+                int32_t forbid_before_step, const int64_t* forbidden_by_row,
+                int32_t row_forbidden_count, int64_t* token_out, float* logprob_out,
+                void* stream) {
+  if (rows < 0 || vocab <= 0 || (row_stride != 0 && row_stride < vocab))
+    return fail(AIOS_ERR_INVALID, "sample: bad sizes (rows=%d vocab=%d stride=%lld)", rows, vocab,
+                (long long)row_stride);
+  if (elem_bytes != 2 && elem_bytes != 4)
+    return fail(AIOS_ERR_UNSUPPORTED, "sample: elem_bytes %d", elem_bytes);
+  if (n_forbidden < 0 || row_forbidden_count < 0 ||
+      n_forbidden + row_forbidden_count > aios::kSampleMaxForbidden)
+    return fail(AIOS_ERR_INVALID, "sample: at most %d forbidden ids per row",
+                aios::kSampleMaxForbidden);
+  const bool greedy = (temperature <= 0.f || top_k == 1) && top_p == 1.f;
+  if (!greedy) {
+    if (!(temperature > 0.f)) return fail(AIOS_ERR_INVALID, "sample: temperature must be positive");
+    if (!(top_p > 0.f && top_p <= 1.f)) return fail(AIOS_ERR_INVALID, "sample: top_p must be in (0, 1]");
+    if (top_k > aios::kSampleMaxTopK)
+      return fail(AIOS_ERR_UNSUPPORTED, "sample: top_k %d above %d is not built", top_k,
+                  aios::kSampleMaxTopK);
+    if (top_k <= 0 && top_p < 1.f)
+      return fail(AIOS_ERR_UNSUPPORTED, "sample: top_p without top_k (a full-vocabulary sort) is not built");
+    if (!uniforms || uniform_count < 1 || uniform_stride < uniform_count)
+      return fail(AIOS_ERR_INVALID, "sample: uniforms are required to sample");
+  }
+  if (rows == 0) return AIOS_OK;
+  if (!logits || !token_out || !logprob_out) return fail(AIOS_ERR_INVALID, "sample: null pointer");
+  if (((uintptr_t)logits & 15) != 0 || (row_stride * elem_bytes) % 16 != 0)
+    return fail(AIOS_ERR_INVALID, "sample: logits rows must be 16-byte aligned");
+  if ((n_forbidden > 0 && !forbidden) || (row_forbidden_count > 0 && !forbidden_by_row))
+    return fail(AIOS_ERR_INVALID, "sample: null forbidden list");
+  aios::SampleArgs a;
+  a.logits = logits;
+  a.row_stride = row_stride;
+  a.rows = rows;
+  a.vocab = vocab;
+  a.elem_bytes = elem_bytes;
+  a.temperature = temperature;
+  a.top_k = greedy ? 1 : (top_k > 0 ? top_k : 0);
+  a.top_p = top_p;
+  a.greedy = greedy ? 1 : 0;
+  a.uniforms = greedy ? nullptr : uniforms;
+  a.uniform_stride = uniform_stride;
+  a.uniform_count = uniform_count;
+  a.step = step;
+  a.forbidden = n_forbidden > 0 ? forbidden : nullptr;
+  a.n_forbidden = n_forbidden;
+  a.forbid_before_step = forbid_before_step;
+  a.forbidden_by_row = row_forbidden_count > 0 ? forbidden_by_row : nullptr;
+  a.row_forbidden_count = row_forbidden_count;
+  a.token_out = token_out;
+  a.logprob_out = logprob_out;
+  return check_hip(aios::sample_rows(a, static_cast<hipStream_t>(stream)), "sample launch");
+}
+
 static bool overlaps(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes) {
   if (!a || !b) return false;
   const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;

@@ -135,6 +135,35 @@ hipError_t greedy_select(const void* logits, int64_t row_stride, int32_t rows, i
                          int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                          hipStream_t stream);
 
+// Stateless candidate sampling (sampling.hip).  One workgroup per row.
+struct SampleArgs {
+  const void* logits;
+  int64_t row_stride;  // elements
+  int32_t rows;
+  int32_t vocab;
+  int32_t elem_bytes;  // 2: bf16, 4: fp32
+  float temperature;
+  int32_t top_k;       // 0: every id (then top_p must be 1)
+  float top_p;
+  int32_t greedy;      // argmax of the sampling logits
+  const float* uniforms;   // u of row r at uniforms[r * uniform_stride + step]
+  int64_t uniform_stride;
+  int32_t uniform_count;   // columns of the table (the step is clamped into them)
+  const int64_t* step;     // device scalar (may be null: step 0)
+  const int32_t* forbidden;  // ids blocked while step < forbid_before_step
+  int32_t n_forbidden;
+  int32_t forbid_before_step;
+  const int64_t* forbidden_by_row;  // [rows][row_forbidden_count] (may be null)
+  int32_t row_forbidden_count;
+  int64_t* token_out;
+  float* logprob_out;
+};
+constexpr int kSampleMaxTopK = 1024;
+constexpr int kSampleMaxForbidden = 256;
+hipError_t sample_rows(const SampleArgs& a, hipStream_t stream);
+hipError_t stateless_uniforms(const int64_t* seeds, int32_t rows, int32_t steps, float* out,
+                              hipStream_t stream);
+
 // Block-AttnRes depth mix (attnres.hip).  bank [bank_sources][num_tokens]
 // [hidden] and every [num_tokens][hidden] plane contiguous bf16.
 struct AttnResArgs {

@@ -299,6 +299,47 @@ int aios_greedy_select(const void* logits, int64_t row_stride, int32_t rows, int
                        void* stream);
 
 /*
+ * out[r][t] = the stateless U(0, 1) of candidate seed seeds[r] at token
+ * step t (fp32 [rows][steps]): SplitMix64 of seed + (t + 1) * 0x9E3779B97F4A7C15,
+ * (high 53 bits + 0.5) / 2^53.  Replaces stateless_uniforms
+ * (python/aios/engine/sample.py:12-47), computed on the device.
+ */
+int aios_stateless_uniforms(const int64_t* seeds, int32_t rows, int32_t steps, float* out,
+                            void* stream);
+
+/*
+ * One token per row of logits (elem_bytes 2: bf16, 4: fp32; rows
+ * row_stride elements apart, 16-byte aligned; row_stride 0: every row
+ * samples the same logits, e.g. the prefix logits of a candidate group,
+ * each with its own uniform) and its raw log-probability
+ * log_softmax(logits)[token] (fp32), as Sampler.sample_with_logprobs with
+ * stateless uniforms (python/aios/engine/sample.py:50-160):
+ *   - sampling logits = logits with the forbidden ids at -inf: forbidden
+ *     (n_forbidden ids, applied while *step < forbid_before_step) and row
+ *     r's forbidden_by_row[r][0 .. row_forbidden_count) (at most 256 ids in
+ *     all; ids outside the vocabulary are ignored);
+ *   - greedy ((temperature <= 0 or top_k == 1) and top_p == 1): the first
+ *     index of the maximum;
+ *   - otherwise logits / temperature; the top_k largest (ties: lower id
+ *     first; top_k <= 1024) or, for top_k <= 0 with top_p == 1, every id in
+ *     id order; softmax; for top_p < 1 the ids whose preceding cumulative
+ *     probability exceeds top_p are removed (the first is kept) and the
+ *     softmax is taken again; the chosen candidate is the number of
+ *     cumulative probabilities below u, clamped to the last one, with u =
+ *     uniforms[r * uniform_stride + min(*step, uniform_count - 1)] (step
+ *     NULL: column 0).
+ * top_k <= 0 with top_p < 1 (a full-vocabulary sort) returns
+ * AIOS_ERR_UNSUPPORTED.  token_out int64, logprob_out fp32, both [rows].
+ */
+int aios_sample(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                int32_t elem_bytes, float temperature, int32_t top_k, float top_p,
+                const float* uniforms, int64_t uniform_stride, int32_t uniform_count,
+                const int64_t* step, const int32_t* forbidden, int32_t n_forbidden,
+                int32_t forbid_before_step, const int64_t* forbidden_by_row,
+                int32_t row_forbidden_count, int64_t* token_out, float* logprob_out,
+                void* stream);
+
+/*
  * Block-AttnRes depth mix.  bank is contiguous bf16 [bank_sources]
  * [num_tokens][hidden]; partial (may be NULL) a contiguous bf16
  * [num_tokens][hidden] plane appended as the last source;

@@ -566,3 +566,87 @@ def test_oracle_attnres_model_matches_product_composition():
     # the mixers matter: the standard trunk on the same weights differs
     std = OracleModel(_tiny_config(num_layers=8), w).logits(ids[None])[0]
     assert not torch.allclose(std, ref, atol=1e-2)
+
+
+# --- stateless candidate sampling --------------------------------------------
+
+from oracle import sampling as osamp  # noqa: E402
+
+
+def test_splitmix64_published_vector():
+    """SplitMix64 (Vigna) with seed 1234567: the first five outputs of the
+    published reference stream; step t of the reference's uniform is the
+    generator's (t + 1)-th output (sample.py:12-21)."""
+    want = [6457827717110365317, 3203168211198807973, 9817491932198370423,
+            4593380528125082431, 16408922859458223821]
+    assert [osamp.splitmix64(1234567, t) for t in range(5)] == want
+
+
+def test_stateless_uniforms_range_and_keying():
+    u = osamp.stateless_uniforms([20260814 + i for i in range(8)], 12)
+    assert u.shape == (8, 12) and u.dtype == np.float32
+    assert (u > 0).all() and (u < 1).all()
+    # keyed by (seed, step), not by row position: candidate 3's stream is the
+    # same wherever it sits in the batch
+    assert np.array_equal(osamp.stateless_uniforms([20260817], 12)[0], u[3])
+    assert abs(float(u.mean()) - 0.5) < 0.1
+    with pytest.raises(ValueError):
+        osamp.stateless_uniforms([1], 0)
+
+
+def test_sample_greedy_is_argmax_with_forbidden():
+    x = np.array([0.1, 3.0, 3.0, -1.0, 2.5])
+    tok, lp, _ = osamp.sample_row(x, 0.0, 0, 1.0, 0.5)
+    assert tok == 1  # first index of the maximum
+    assert np.isclose(lp, x[1] - np.log(np.exp(x).sum()))
+    tok, lp, _ = osamp.sample_row(x, 0.7, 1, 1.0, 0.5, forbidden=[1, 2])
+    assert tok == 4
+    assert np.isclose(lp, x[4] - np.log(np.exp(x).sum()))  # raw, unmodified distribution
+
+
+def test_sample_full_vocab_is_inverse_cdf():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(50) * 2
+    t = 0.8
+    p = np.exp(x / t - (x / t).max())
+    p /= p.sum()
+    cum = np.cumsum(p)
+    for u in rng.uniform(0, 1, 200):
+        tok, _, _ = osamp.sample_row(x, t, 0, 1.0, u)
+        assert tok == min(int(np.searchsorted(cum, u, side="left")), len(x) - 1)
+
+
+def test_sample_top_p_known_answer():
+    """probs [0.5, 0.3, 0.15, 0.05], top_p 0.7: cumulative [0.5, 0.8, ...]
+    removes ids 2 and 3 (the cumulative before them exceeds 0.7); the kept
+    pair renormalises to [0.625, 0.375]."""
+    x = np.log(np.array([0.5, 0.3, 0.15, 0.05]))
+    assert osamp.sample_row(x, 1.0, 0, 0.7, 0.6)[0] == 0
+    assert osamp.sample_row(x, 1.0, 0, 0.7, 0.63)[0] == 1
+    assert osamp.sample_row(x, 1.0, 0, 0.7, 0.99)[0] == 1
+    assert osamp.sample_row(x, 1.0, 4, 0.7, 0.99)[0] == 1  # same with top_k covering all
+
+
+def test_sample_frequencies_match_truncated_distribution():
+    """top_k 3 of 6 at temperature 0.5: over a fine u grid each candidate is
+    drawn with its renormalised probability; the others never."""
+    x = np.array([1.0, -0.5, 2.0, 0.3, 1.9, -2.0])
+    s = x / 0.5
+    top = np.argsort(-s)[:3]
+    p = np.exp(s[top] - s[top].max())
+    p /= p.sum()
+    grid = (np.arange(20000) + 0.5) / 20000
+    counts = {}
+    for u in grid:
+        tok = osamp.sample_row(x, 0.5, 3, 1.0, u)[0]
+        counts[tok] = counts.get(tok, 0) + 1
+    assert set(counts) == set(top.tolist())
+    for i, t in enumerate(top):
+        assert abs(counts[int(t)] / len(grid) - p[i]) < 1e-3
+
+
+def test_sample_ties_take_lower_id_first():
+    x = np.array([0.0, 5.0, 1.0, 5.0, 5.0])
+    # three-way tie at the top: top_k 2 keeps ids 1 and 3, in that order
+    assert osamp.sample_row(x, 1.0, 2, 1.0, 0.25)[0] == 1
+    assert osamp.sample_row(x, 1.0, 2, 1.0, 0.75)[0] == 3
