@@ -14,12 +14,19 @@ Restates the GPU control flow of ImeCompletionEngine (python/aios/ime.py):
     use after complete() equal the prefix length (tests/test_ime_gpu.py:36);
   * KV budget check (:467-478) and latest-wins cancellation observed once per
     decode step (:174-184, :971-973).
-Text governance and sampling are not restated (no tokenizer ships with the
-synthetic models): candidate i starts from the i-th most likely first token
-and then decodes greedily (argmax of the logits, with the raw log-prob of
-the chosen token, sample.py:73, 115-117, on the device kernel
-aios_greedy_select); candidates are ranked by average raw log-prob (the
-reference's base score before text penalties, :1109-1115).
+Candidate rule.  With ``CandidateGroupConfig.sampling`` set, the
+reference's: candidate i draws every token, the first one from the prefix
+logits included, with temperature / top-k / top-p from its own stateless
+uniform stream keyed by (seed + i, token step), with the blocked ids
+(EOS and terminal ids) forbidden before ``min_new_tokens``
+(ime.py:891-1008, sample.py:12-160, on the device kernels aios_sample and
+aios_stateless_uniforms).  Without it (the greedy configurations),
+candidate i starts from the i-th most likely first token and then decodes
+greedily (aios_greedy_select).  Either way each token's raw log-prob is
+kept and candidates are ranked by average raw log-prob (the reference's
+base score before text penalties, :1109-1115).  Text governance and
+refill rounds are not restated (no tokenizer ships with the synthetic
+models).
 """
 from __future__ import annotations
 
@@ -31,6 +38,7 @@ import torch
 
 from aios_amd.config import ModelConfig
 from aios_amd.core import Batch, Context, Req, SamplingParams, reset_global_ctx, set_global_ctx
+from aios_amd.sample import sample_step, stateless_uniforms
 from aios_amd.kvcache import MHAKVCache
 from aios_amd.paged import greedy_select
 from aios_amd.minimind_ime import build_causal_lm
@@ -68,12 +76,28 @@ class CandidateGroupConfig:
     max_new_tokens: int = 16
     display_candidates: int = 3
     eos_token_id: int | None = None
+    # None: greedy candidates from the top first tokens.  Otherwise the
+    # reference's sampled candidates (ImeGenerationConfig defaults:
+    # temperature 0.35, top_k 50, top_p 0.9, seed 20260814, ime.py:33-56).
+    sampling: SamplingParams | None = None
+    seed: int = 20260814
+    min_new_tokens: int = 0
+    blocked_token_ids: tuple[int, ...] = ()  # with EOS: forbidden before min_new_tokens
 
     def validate(self) -> None:
         if self.num_candidates < self.display_candidates or self.display_candidates < 1:
             raise ValueError("num_candidates must cover display_candidates")
         if self.max_new_tokens < 1:
             raise ValueError("max_new_tokens must be positive")
+        if self.min_new_tokens < 0:
+            raise ValueError("min_new_tokens must be non-negative")
+
+    def blocked_ids(self) -> tuple[int, ...]:
+        """ime.py:948-955: terminal ids and EOS, blocked before min_new_tokens."""
+        ids = set(int(t) for t in self.blocked_token_ids)
+        if self.eos_token_id is not None:
+            ids.add(int(self.eos_token_id))
+        return tuple(sorted(ids))
 
 
 @dataclass(frozen=True)
@@ -309,11 +333,26 @@ class CandidateGroupEngine:
         logp_sum = torch.zeros(n, dtype=torch.float32, device=dev)
         counts = torch.zeros(n, dtype=torch.long, device=dev)
         eos_hit = torch.zeros(n, dtype=torch.bool, device=dev)
-        # First token of candidate i: the i-th most likely continuation.
-        lp0 = torch.log_softmax(prefix_logits[0].float(), dim=-1)
-        top = torch.topk(lp0, n)
-        token = top.indices
-        raw_lp = top.values
+        sampled = config.sampling is not None
+        if sampled:
+            uni = stateless_uniforms([config.seed + i for i in range(n)], t_max, dev)
+            blocked = config.blocked_ids()
+            blocked_t = (torch.tensor(blocked, dtype=torch.int32, device=dev) if blocked
+                         else None)
+
+            def pick(logits, rows, step):
+                col = torch.full((1,), step, dtype=torch.int64, device=dev)
+                return sample_step(logits, config.sampling, uni[rows], col, blocked_t,
+                                   config.min_new_tokens)
+
+            # every candidate draws its first token from the prefix logits
+            token, raw_lp = pick(prefix_logits[:1].expand(n, -1), torch.arange(n, device=dev), 0)
+        else:
+            # First token of candidate i: the i-th most likely continuation.
+            lp0 = torch.log_softmax(prefix_logits[0].float(), dim=-1)
+            top = torch.topk(lp0, n)
+            token = top.indices
+            raw_lp = top.values
         active = list(range(n))
         allocated = []
         cancelled = False
@@ -322,9 +361,9 @@ class CandidateGroupEngine:
             if cancellation.cancelled:  # observed between steps (ime.py:971-973)
                 cancelled = True
                 break
-            if step:
-                token, raw_lp = greedy_select(logits)
             act = torch.tensor(active, dtype=torch.long, device=dev)
+            if step:
+                token, raw_lp = pick(logits, act, step) if sampled else greedy_select(logits)
             emitted = torch.ones_like(token, dtype=torch.bool)
             if config.eos_token_id is not None:
                 emitted = token.ne(config.eos_token_id)
@@ -368,17 +407,20 @@ class CandidateGroupEngine:
         # multiple of 64, so neighbouring prefix lengths share one graph.
         plan_prefix = (prefix_len // 64) * 64
         kv_cap = min(-(-(prefix_len + t_max) // 64) * 64, self.rt.max_context)
-        key = (n, t_max, plan_prefix, kv_cap, config.eos_token_id)
+        sp = config.sampling
+        key = (n, t_max, plan_prefix, kv_cap, config.eos_token_id,
+               None if sp is None else (sp.temperature, sp.top_k, sp.top_p),
+               config.min_new_tokens, config.blocked_ids())
         g = self._graphs.get(key)
         if g is None:
-            g = _DecodeGraph(self, n, t_max, plan_prefix, kv_cap, config.eos_token_id)
+            g = _DecodeGraph(self, n, t_max, plan_prefix, kv_cap, config.eos_token_id, config)
             self._graphs[key] = g
         allocated = []
         if t_max > 1:
             pages = self.rt.cache_manager.allocate(n * (t_max - 1))
             allocated.append(pages)
             g.pages[: t_max - 1].copy_(pages.view(t_max - 1, n))
-        g.start(prefix_logits, prefix_len)
+        g.start(prefix_logits, prefix_len, config.seed)
         cancelled = False
         for _ in range(t_max - 1):
             if cancellation.cancelled:  # observed between steps (ime.py:971-973)
@@ -411,13 +453,21 @@ class _DecodeGraph:
     """
 
     def __init__(self, eng: "CandidateGroupEngine", rows: int, steps: int, plan_prefix: int,
-                 kv_cap: int, eos: int | None) -> None:
+                 kv_cap: int, eos: int | None, config: CandidateGroupConfig) -> None:
         rt = eng.rt
         dev = rt.device
         self.rt = rt
         self.rows = rows
         self.steps = steps
         self.eos = eos
+        # sampled candidates: the group's uniform table (refilled per group),
+        # the ids blocked before min_new_tokens
+        self.sampling = config.sampling
+        self.min_new = config.min_new_tokens
+        blocked = config.blocked_ids()
+        self.blocked = (torch.tensor(blocked, dtype=torch.int32, device=dev) if blocked
+                        else None)
+        self.uni = torch.zeros((rows, steps), dtype=torch.float32, device=dev)
         self.tokens = torch.zeros(rows, dtype=torch.long, device=dev)
         self.pos = torch.zeros(rows, dtype=torch.int32, device=dev)
         self.step = torch.zeros(1, dtype=torch.long, device=dev)
@@ -440,16 +490,26 @@ class _DecodeGraph:
         self.batch.attn_metadata = self.md
         self.graph: torch.cuda.CUDAGraph | None = None
 
-    def start(self, prefix_logits: torch.Tensor, prefix_len: int) -> None:
-        """Step 0: candidate i takes the i-th most likely first token."""
-        lp0 = torch.log_softmax(prefix_logits[0].float(), dim=-1)
-        top = torch.topk(lp0, self.rows)
-        tok = top.indices
+    def start(self, prefix_logits: torch.Tensor, prefix_len: int, seed: int) -> None:
+        """Step 0: candidate i samples the prefix logits with its own uniform
+        stream (sampled candidates), or takes the i-th most likely first
+        token (greedy candidates)."""
+        if self.sampling is not None:
+            dev = self.rt.device
+            self.uni.copy_(stateless_uniforms([seed + i for i in range(self.rows)], self.steps,
+                                              dev))
+            col = torch.zeros(1, dtype=torch.int64, device=dev)
+            tok, val = sample_step(prefix_logits[:1].expand(self.rows, -1), self.sampling,
+                                   self.uni, col, self.blocked, self.min_new)
+        else:
+            lp0 = torch.log_softmax(prefix_logits[0].float(), dim=-1)
+            top = torch.topk(lp0, self.rows)
+            tok, val = top.indices, top.values
         emitted = torch.ones_like(tok, dtype=torch.bool) if self.eos is None else tok.ne(self.eos)
         self.tokens.copy_(tok)
         self.out_ids.fill_(-1)
         self.out_ids[:, 0] = torch.where(emitted, tok, torch.full_like(tok, -1))
-        self.logp_sum.copy_(torch.where(emitted, top.values, torch.zeros_like(top.values)))
+        self.logp_sum.copy_(torch.where(emitted, val, torch.zeros_like(val)))
         self.counts.copy_(emitted.long())
         self.finished.copy_(~emitted)
         self.eos_hit.copy_(~emitted)
@@ -465,7 +525,11 @@ class _DecodeGraph:
         self.batch.out_loc = out_loc
         with rt.ctx.forward_batch(self.batch):
             logits = rt.model.forward()
-        tok, raw = greedy_select(logits)
+        if self.sampling is not None:
+            tok, raw = sample_step(logits, self.sampling, self.uni, self.step + 1, self.blocked,
+                                   self.min_new)
+        else:
+            tok, raw = greedy_select(logits)
         live = ~self.finished
         self.fed += live.sum()
         emitted = live if self.eos is None else live & tok.ne(self.eos)

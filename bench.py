@@ -15,7 +15,9 @@ Prints one JSON line: value = decode-step microseconds (lower is better),
 with the main decode kernel's roofline measured live with HIP events, the
 full-model CandidateGroup Top-3 latency of the MiniMind-0.1B-shaped model
 (``candidate_group``: p50/p95 over 30 seeded prefixes after 5 warmups, with
-graph-replayed and eager decode steps) and of the Qwen3-0.6B-shaped model
+graph-replayed and eager decode steps; ``candidate_group_sampled``: the same
+model with the reference's default sampled candidates, temperature 0.35,
+top_k 50, top_p 0.9, 12 tokens) and of the Qwen3-0.6B-shaped model
 on a 128-token prefix extended by 2 ids (``candidate_group_qwen3_0p6b``:
 the cross-keystroke case, 8 candidates x 24 steps) and of the 0.214B
 Block-AttnRes-shaped model (``candidate_group_attnres_0p214b``: 64-token
@@ -170,7 +172,8 @@ def prefix_prefill(seed: int, reps: int = 10) -> dict:
 
 
 def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int = 32,
-                    steps: int = 16, extend: int = 0, runs: int = 30, warmups: int = 5) -> dict:
+                    steps: int = 16, extend: int = 0, runs: int = 30, warmups: int = 5,
+                    sampling: tuple | None = None, min_new_tokens: int = 0) -> dict:
     """Full CandidateGroup Top-3 latency of a synthetic-weight model.
 
     Default: the MiniMind-0.1B-shaped model (14 layers, hidden 768, 8q/2kv
@@ -183,25 +186,35 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int 
     complete() on the prefix extended by `extend` ids, which prefills only
     those ids against the cached prefix KV (token-LCP reuse, ime.py:1116-1168).
     ``warmups`` runs on other prefixes come first (the first one captures the
-    decode-step graph); each run starts from an empty prefix cache.
+    decode-step graph); each run starts from an empty prefix cache.  With
+    ``sampling`` = (temperature, top_k, top_p) the candidates are sampled
+    with stateless uniforms (the reference's candidate rule) instead of
+    greedy from the top first tokens.
     """
     import statistics
 
     import torch
 
     from aios_amd.config import MODELS
-    from aios_amd.core import reset_global_ctx
+    from aios_amd.core import SamplingParams, reset_global_ctx
     from aios_amd.ime import CandidateGroupConfig, CandidateGroupEngine, CandidateGroupRuntime
     from aios_amd.qwen3 import init_weights
 
     c = MODELS[model]
     rt = CandidateGroupRuntime(c, init_weights(c, seed, "cuda"), "cuda", num_pages=2048)
-    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=steps)
+    sp = None if sampling is None else SamplingParams(temperature=sampling[0], top_k=sampling[1],
+                                                      top_p=sampling[2])
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=steps, sampling=sp, seed=seed,
+                               min_new_tokens=min_new_tokens)
     out = {"model": f"{model}-shaped ({c.num_layers}L, {c.hidden_size}, "
                     f"{c.num_qo_heads}q/{c.num_kv_heads}kv x {c.head_dim}, "
                     f"ffn {c.intermediate_size}, vocab {c.vocab_size})",
            "prefix_tokens": prefix_tokens, "extend_tokens": extend, "candidates": 8,
-           "decode_steps": steps, "runs": runs, "warmups": warmups}
+           "decode_steps": steps, "runs": runs, "warmups": warmups,
+           "candidates_rule": ("greedy from the top first tokens" if sp is None else
+                               f"sampled: temperature {sp.temperature}, top_k {sp.top_k}, "
+                               f"top_p {sp.top_p}, stateless uniforms, min_new_tokens "
+                               f"{min_new_tokens}")}
     for mode in ("graph", "eager"):
         eng = CandidateGroupEngine(rt, use_graphs=mode == "graph")
         lat, gpu, gen = [], [], 0
@@ -534,6 +547,10 @@ def main() -> int:
         _log(f"candidate group {result['candidate_group']['graph']['top3_p50_ms']} ms p50")
         # Qwen3-0.6B-shaped: 128-token prefix extended by 2 ids (cross-keystroke
         # reuse), 8 candidates x 24 steps.
+        result["candidate_group_sampled"] = candidate_group(
+            args.seed, steps=12, sampling=(0.35, 50, 0.9), min_new_tokens=2)
+        _log(f"candidate group sampled {result['candidate_group_sampled']['graph']['top3_p50_ms']} "
+             "ms p50")
         result["candidate_group_qwen3_0p6b"] = candidate_group(
             args.seed, model="qwen3-0.6b", prefix_tokens=128, steps=24, extend=2, runs=20,
             warmups=3)

@@ -37,6 +37,13 @@
  *                      the logits plus the raw log_softmax value gathered
  *                      there, as called by the CandidateGroup decode loop
  *                      (python/aios/ime.py:998-1008)
+ *   aios_stateless_uniforms, aios_sample  stateless_uniforms and the
+ *                      uniforms path of Sampler.sample_with_logprobs
+ *                      (python/aios/engine/sample.py:12-160)
+ *   aios_attnres_mix, aios_attnres_mix_ex  triton_attnres_mix
+ *                      (python/aios/kernel/attnres.py:130-223) behind
+ *                      BlockAttnResMixer (python/aios/models/minimind_ime.py:
+ *                      92-190), the latter with the block's partial update
  */
 #ifndef AIOS_ATTN_H
 #define AIOS_ATTN_H

@@ -366,3 +366,83 @@ def test_graph_replay_matches_eager_attnres():
             [x.average_logprob for x in e.raw_candidates]
         _check_against_oracle(g, om, prefix, 8, 10)
     assert rt.cache_manager.available_size == rt.num_pages
+
+
+# --- sampled candidates (the reference's default candidate rule) ------------
+
+from aios_amd.core import SamplingParams  # noqa: E402
+from oracle import sampling as osamp  # noqa: E402
+
+
+def _check_sampled(res, prefix_logits, rec, cfg, n):
+    """Every token of every candidate is what the sampling oracle draws from
+    the GPU's own logits of that step with the candidate's stateless uniform
+    (boundary cases: within 1e-5 of a cumulative sum, either neighbour)."""
+    sp = cfg.sampling
+    uni = osamp.stateless_uniforms([cfg.seed + i for i in range(n)], cfg.max_new_tokens)
+    blocked = list(cfg.blocked_ids())
+    steps = [(list(range(n)), prefix_logits.float().cpu().expand(n, -1))] + \
+        [(rows, lg) for rows, lg in rec]
+    checked = 0
+    for j, (rows, lg) in enumerate(steps):
+        for local, cand in enumerate(rows):
+            tok = res.raw_candidates[cand].token_ids[j]
+            fb = blocked if j < cfg.min_new_tokens else []
+            want, _, d = osamp.sample_row(lg[local].numpy(), sp.temperature, sp.top_k, sp.top_p,
+                                          float(uni[cand, j]), fb, detail=True)
+            assert tok not in fb
+            if d["u_margin"] > 1e-5 and d["cut_margin"] > 1e-5:
+                assert tok == want, (j, cand, tok, want)
+                checked += 1
+            else:
+                assert tok in set(d["order"].tolist())
+    assert checked >= 0.9 * n * cfg.max_new_tokens
+
+
+def test_candidate_group_sampled_minimind_0p1b():
+    """The reference's first-round rule (temperature 0.35, top_k 50, top_p
+    0.9, stateless uniforms keyed by seed + candidate), eager steps."""
+    c = MINIMIND_0P1B
+    eng, om = _engine(c, 20260814)
+    prefix = _prefix(20260814, 32, c.vocab_size)
+    rec = _record_decode_logits(eng)
+    first = eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=1))
+    top2 = first.prefix_logits[0].float().topk(2).indices.tolist()
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=12,
+                               sampling=SamplingParams(temperature=0.35, top_k=50, top_p=0.9),
+                               min_new_tokens=2, blocked_token_ids=tuple(top2))
+    rec.clear()
+    res = eng.complete(prefix, cfg)
+    assert len(res.raw_candidates) == 8
+    assert all(len(cand.token_ids) == 12 for cand in res.raw_candidates)
+    _check_sampled(res, res.prefix_logits, rec, cfg, 8)
+    # the two most likely first tokens are blocked for the first two steps
+    assert all(cand.token_ids[0] not in top2 for cand in res.raw_candidates)
+    # raw scores are the unmodified distribution's log-probs (oracle model)
+    ids = torch.tensor([cand.token_ids for cand in res.raw_candidates])
+    tf = om.teacher_forced(prefix, ids)
+    avg_ref = tf.gather(2, ids[:, :, None]).squeeze(2).mean(1)
+    avg_gpu = torch.tensor([cand.average_logprob for cand in res.raw_candidates])
+    assert (avg_ref - avg_gpu).abs().max().item() <= AVG_LP_TOL
+
+
+def test_graph_replay_matches_eager_sampled():
+    c = MINIMIND_0P1B.with_layers(4)
+    w = init_weights(c, 8, "cpu")
+    rt = CandidateGroupRuntime(c, weights_to(w, "cuda"), "cuda", num_pages=1024)
+    eager = CandidateGroupEngine(rt, use_graphs=False)
+    graphed = CandidateGroupEngine(rt, use_graphs=True)
+    for seed in (1, 2, 1):
+        cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=10, seed=100 + seed,
+                                   sampling=SamplingParams(temperature=0.75, top_k=96, top_p=0.95),
+                                   min_new_tokens=2, blocked_token_ids=(3, 4))
+        prefix = _prefix(seed, 32, c.vocab_size)
+        e = eager.complete(prefix, cfg)
+        eager.reset_prefix_cache()
+        torch.cuda.synchronize()
+        g = graphed.complete(prefix, cfg)
+        graphed.reset_prefix_cache()
+        assert [x.token_ids for x in g.raw_candidates] == [x.token_ids for x in e.raw_candidates]
+        assert [x.average_logprob for x in g.raw_candidates] == \
+            [x.average_logprob for x in e.raw_candidates]
+    assert len(graphed._graphs) == 1
