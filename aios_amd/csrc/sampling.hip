@@ -7,8 +7,10 @@
 // logits as stored (torch's argmax on the sampling logits); logprob =
 // x[token] - logsumexp(x) in fp32 (log_softmax of the fp32-widened logits,
 // gathered at the token).  Each lane keeps an online (max, first index,
-// sum of exp(x - max)) state over a strided slice of the row; states merge
-// across the wavefront with shuffles and across waves through LDS.
+// sum of exp(x - max)) state over its 8-logit chunks of the row (several
+// 16-byte loads in flight: the row is read in a few memory round trips, not
+// one per 256 logits); states merge across the wavefront with shuffles and
+// across waves through LDS.
 #include "kernels.hpp"
 
 namespace aios {
@@ -42,6 +44,20 @@ __device__ __forceinline__ float load_logit(const T* p) {
   return static_cast<float>(*p);
 }
 
+// Eight consecutive logits (16-byte aligned) as fp32.
+__device__ __forceinline__ void load8f(const bf16* p, float* f) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  f[0] = lo_bf16(v.x); f[1] = hi_bf16(v.x); f[2] = lo_bf16(v.y); f[3] = hi_bf16(v.y);
+  f[4] = lo_bf16(v.z); f[5] = hi_bf16(v.z); f[6] = lo_bf16(v.w); f[7] = hi_bf16(v.w);
+}
+__device__ __forceinline__ void load8f(const float* p, float* f) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
+constexpr int kGreedyUnroll = 4;  // 8-logit chunks per thread in flight
+
 template <typename T>
 __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
     const T* __restrict__ logits, int64_t row_stride, int32_t vocab,
@@ -49,8 +65,8 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
   const int row = blockIdx.x;
   const T* x = logits + (int64_t)row * row_stride;
   ArgState st = {kNegInf, 0x7fffffff, 0.f};
-  for (int32_t j = threadIdx.x; j < vocab; j += kGreedyThreads) {
-    const float v = load_logit(x + j) * kLog2e;
+  auto visit = [&](float v, int32_t j) {
+    v *= kLog2e;
     if (v > st.m) {
       st.s = (st.m == kNegInf ? 0.f : st.s * fast_exp2(st.m - v)) + 1.f;
       st.m = v;
@@ -58,7 +74,28 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
     } else if (v != kNegInf) {
       st.s += fast_exp2(v - st.m);
     }
+  };
+  // Whole 8-logit chunks with several 16-byte loads in flight per thread
+  // (unconditional: a chunk past the last whole one re-reads that one and
+  // is skipped), then the rest one by one.  Each thread visits its ids in
+  // increasing order, so its state keeps the first index of its maximum.
+  const int whole = ((uintptr_t)x & 15) == 0 ? (vocab & ~7) : 0;
+  for (int base = 0; base < whole; base += kGreedyThreads * 8 * kGreedyUnroll) {
+    float f[kGreedyUnroll][8];
+    int i0[kGreedyUnroll];
+#pragma unroll
+    for (int u = 0; u < kGreedyUnroll; ++u) {
+      i0[u] = base + (u * kGreedyThreads + (int)threadIdx.x) * 8;
+      load8f(x + min(i0[u], whole - 8), f[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kGreedyUnroll; ++u)
+      if (i0[u] < whole) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) visit(f[u][j], i0[u] + j);
+      }
   }
+  for (int32_t j = whole + threadIdx.x; j < vocab; j += kGreedyThreads) visit(load_logit(x + j), j);
   for (int off = 32; off > 0; off >>= 1) {
     ArgState o;
     o.m = __shfl_xor(st.m, off);
@@ -104,6 +141,12 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
 constexpr int kSampleThreads = 256;
 constexpr int kSampleWaves = kSampleThreads / 64;
 constexpr int kSampleTile = kSampleThreads * 8;
+constexpr int kSampleUnroll = 8;  // 16-byte chunks per thread in flight per sweep
+// candidates (ids at or above the k-th key) gathered without order; more
+// ties than fit take the id-ordered gather instead
+constexpr int kSampleGatherCap = 2048;
+constexpr int kSampleRankSort = 1024;
+static_assert(kSampleGatherCap >= kSampleMaxTopK, "the sorted buffer holds the top k");
 
 // Order-preserving keys: larger value <=> larger key.
 __device__ __forceinline__ uint32_t order_key32(uint32_t b) {
@@ -185,7 +228,9 @@ struct SampleShared {
   float fred[kSampleWaves][2];
   int iscan[kSampleWaves];
   float fscan[kSampleWaves];
-  unsigned long long cand[kSampleMaxTopK];
+  int ngather;
+  unsigned long long cand[kSampleGatherCap];
+  unsigned long long top[kSampleMaxTopK];  // the k winners, in order
 };
 
 template <typename T>
@@ -243,129 +288,115 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
     }
   };
 
+  // Every id of the row once, in no particular order, with kSampleUnroll
+  // 16-byte loads per thread issued before any is used (a load per
+  // iteration would make each sweep one memory round trip per 2048 ids).
+  // The loads are unconditional: a chunk past the last whole one re-reads
+  // that one and is masked; the (< 8) ids past the last whole chunk are
+  // read one by one.
+  const int whole = vocab & ~7;
+  auto sweep = [&](auto&& f) {
+    for (int base = 0; base < whole; base += kSampleTile * kSampleUnroll) {
+      uint32_t bits[kSampleUnroll][8];
+      int i0[kSampleUnroll];
+#pragma unroll
+      for (int u = 0; u < kSampleUnroll; ++u) {
+        i0[u] = base + (u * kSampleThreads + tid) * 8;
+        L::load8(x + min(i0[u], whole - 8), bits[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kSampleUnroll; ++u) {
+        if (i0[u] < whole) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) f(i0[u] + j, bits[u][j]);
+        }
+      }
+    }
+    for (int i = whole + tid; i < vocab; i += kSampleThreads) f(i, L::load1(x + i));
+  };
+
   const bool full_vocab = !a.greedy && a.top_k == 0;
   const int k = a.greedy ? 1 : min(a.top_k, vocab);
 
-  // Raw log-sum-exp (natural log) state of this thread, and for the
-  // full-vocabulary mode the sampling maximum.
-  float rm = kNegInf, rs = 0.f, smax = kNegInf;
-  uint32_t pref = 0;
-  int krem = k;
-  for (int pass = 0; pass < (full_vocab ? 1 : kPasses); ++pass) {
-    const int shift = L::kBits - 4 * (pass + 1);
-    const uint32_t hi_mask = pass == 0 ? 0u : ((~0u << (shift + 4)) & (L::kBits == 16 ? 0xffffu : ~0u));
-    int cnt[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) cnt[j] = 0;
-    for (int t0 = 0; t0 < vocab; t0 += kSampleTile) {
-      const int i0 = t0 + tid * 8;
-      if (i0 >= vocab) continue;
-      uint32_t bits[8];
-      bool ok[8];
-      tile8(i0, bits, ok);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (!ok[j]) continue;
-        if (pass == 0) {
-          const float v = L::to_float(bits[j]);
-          if (v > rm) {
-            rs = (rm == kNegInf ? 0.f : rs * expf(rm - v)) + 1.f;
-            rm = v;
-          } else if (v != kNegInf) {
-            rs += expf(v - rm);
-          }
-          if (full_vocab && v > smax && !forbidden_id(i0 + j)) smax = v;
-        }
-        if (!full_vocab) {
-          const uint32_t key = L::key(bits[j]);
-          if ((key & hi_mask) == pref) {
-            const int d = (key >> shift) & 15;
-            cnt[0] += 1;
-#pragma unroll
-            for (int q = 1; q < 16; ++q) cnt[q] += d >= q ? 1 : 0;
-          }
-        }
-      }
-    }
-    if (full_vocab) break;
-    // block totals of the 16 counters
-#pragma unroll
-    for (int j = 0; j < 16; ++j) cnt[j] = wave_sum_i(cnt[j]);
-    if (lane == 0) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) sh.ired[pass & 1][wave][j] = cnt[j];
-    }
+  // Block reductions through LDS (every thread gets the result).
+  auto block_max = [&](float v) {
+    for (int off = 32; off > 0; off >>= 1) v = vmax(v, __shfl_xor(v, off));
     __syncthreads();
+    if (lane == 0) sh.fscan[wave] = v;
+    __syncthreads();
+    float r = kNegInf;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      int t = 0;
+    for (int w = 0; w < kSampleWaves; ++w) r = vmax(r, sh.fscan[w]);
+    return r;
+  };
+  auto block_sum = [&](float v) {
+    v = wave_sum_f(v);
+    __syncthreads();
+    if (lane == 0) sh.fscan[wave] = v;
+    __syncthreads();
+    float r = 0.f;
 #pragma unroll
-      for (int w = 0; w < kSampleWaves; ++w) t += sh.ired[pass & 1][w][j];
-      cnt[j] = t;
-    }
-    // forbidden ids count at the -inf key
-    for (int f = 0; f < nf; ++f) {
-      const uint32_t rk = sh.fkey[f];
-      if (rk == neg_key) continue;
-      if ((rk & hi_mask) == pref) {
-        const int d = (rk >> shift) & 15;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) cnt[q] -= d >= q ? 1 : 0;
-      }
-      if ((neg_key & hi_mask) == pref) {
-        const int d = (neg_key >> shift) & 15;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) cnt[q] += d >= q ? 1 : 0;
-      }
-    }
-    // largest digit whose ids (with this prefix) number at least krem
-    // (q = 0 always qualifies: cnt[0] >= krem by construction)
-    int dstar = 0, above = 0;
-    bool found = false;
-#pragma unroll
-    for (int q = 15; q >= 0; --q) {
-      const int c_next = q == 15 ? 0 : cnt[q + 1];
-      if (!found && cnt[q] >= krem) {
-        found = true;
-        dstar = q;
-        above = c_next;
-      }
-    }
-    krem -= above;
-    pref |= (uint32_t)dstar << shift;
-  }
+    for (int w = 0; w < kSampleWaves; ++w) r += sh.fscan[w];
+    return r;
+  };
 
-  // raw log-sum-exp over the block
+  // 2a. maxima of the raw logits and of the sampling logits (a forbidden id
+  // is looked up only when its value beats the thread's running maximum)
+  float rmax = kNegInf, smax = kNegInf;
+  sweep([&](int id, uint32_t bits) {
+    const float v = L::to_float(bits);
+    rmax = vmax(rmax, v);
+    if (v > smax && !(nf > 0 && forbidden_id(id))) smax = v;
+  });
+  rmax = block_max(rmax);
+  smax = block_max(smax);
+
+  // 2b. the raw sum of exp (log-sum-exp of the unmodified logits), and how
+  // many sampling logits lie within each window W of their maximum: the
+  // smallest window holding k of them holds the whole top k (ties at the
+  // k-th value included), so it is gathered and sorted instead of found
+  // by radix selection.  W = 0 is the greedy case (the ids at the maximum).
+  constexpr int kWin = 16;
+  float thr[kWin];
   {
-    float m = rm;
-    for (int off = 32; off > 0; off >>= 1) m = vmax(m, __shfl_xor(m, off));
-    float s = rm == kNegInf ? 0.f : rs * expf(rm - m);
-    s = wave_sum_f(s);
-    float sm = smax;
-    for (int off = 32; off > 0; off >>= 1) sm = vmax(sm, __shfl_xor(sm, off));
-    __syncthreads();
-    if (lane == 0) {
-      sh.fred[wave][0] = m;
-      sh.fred[wave][1] = s;
-      sh.fscan[wave] = sm;
-    }
-    __syncthreads();
-    float bm = kNegInf, bsm = kNegInf;
+    const float wins[kWin] = {0.f,  0.125f, 0.25f, 0.5f, 0.75f, 1.f,  1.5f,  2.f,
+                              3.f,  4.f,    6.f,   8.f,  12.f,  16.f, 32.f,  __builtin_inff()};
 #pragma unroll
-    for (int w = 0; w < kSampleWaves; ++w) {
-      bm = vmax(bm, sh.fred[w][0]);
-      bsm = vmax(bsm, sh.fscan[w]);
-    }
-    float bs = 0.f;
+    for (int i = 0; i < kWin; ++i) thr[i] = smax - wins[i];
+  }
+  float rsum = 0.f;
+  int wc[kWin];
 #pragma unroll
-    for (int w = 0; w < kSampleWaves; ++w)
-      bs += sh.fred[w][0] == kNegInf ? 0.f : sh.fred[w][1] * expf(sh.fred[w][0] - bm);
-    rm = bm;
-    rs = bs;
-    smax = bsm;
+  for (int i = 0; i < kWin; ++i) wc[i] = 0;
+  sweep([&](int id, uint32_t bits) {
+    const float v = L::to_float(bits);
+    rsum += fast_exp2((v - rmax) * kLog2e);
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) wc[i] += v >= thr[i] ? 1 : 0;
+  });
+  rsum = block_sum(rsum);
+#pragma unroll
+  for (int i = 0; i < kWin; ++i) wc[i] = wave_sum_i(wc[i]);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) sh.ired[0][wave][i] = wc[i];
   }
   __syncthreads();
-  const float log_z = rm + logf(rs);
+#pragma unroll
+  for (int i = 0; i < kWin; ++i) {
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < kSampleWaves; ++w) t += sh.ired[0][w][i];
+    wc[i] = t;
+  }
+  __syncthreads();
+  // a forbidden id counts at -inf, not at its value
+  for (int f = 0; f < nf; ++f) {
+    const float vf = L::value(sh.fkey[f]);
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) wc[i] += (kNegInf >= thr[i] ? 1 : 0) - (vf >= thr[i] ? 1 : 0);
+  }
+  const float log_z = rmax + logf(rsum);
   // the step's column, clamped into the table the caller passed
   const int64_t col = step < 0 ? 0 : (step >= a.uniform_count ? a.uniform_count - 1 : step);
   const float u = a.uniforms != nullptr ? a.uniforms[(int64_t)row * a.uniform_stride + col] : 0.5f;
@@ -446,84 +477,216 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
     }
     chosen = min(below, vocab - 1);
   } else {
-    // 3. gather the k winners in id order
+    // 3. the candidates
+    int win = -1;
+#pragma unroll
+    for (int i = kWin - 1; i >= 0; --i)
+      if (wc[i] >= k) win = i;
+    int n_sort;
+    if (win >= 0 && wc[win] <= kSampleGatherCap) {
+      // every sampling logit within the smallest window holding k of them
+      float t = thr[0];
+#pragma unroll
+      for (int i = 1; i < kWin; ++i)
+        if (i == win) t = thr[i];
+      if (tid == 0) sh.ngather = 0;
+      __syncthreads();
+      sweep([&](int id, uint32_t bits) {
+        if (!(L::to_float(bits) >= t)) return;
+        uint32_t kk = L::key(bits);
+        if (nf > 0 && forbidden_id(id)) {
+          if (!(kNegInf >= t)) return;
+          kk = neg_key;
+        }
+        const int slot = atomicAdd(&sh.ngather, 1);
+        if (slot < kSampleGatherCap)
+          sh.cand[slot] = ((unsigned long long)kk << 32) | (0xffffffffu - (uint32_t)id);
+      });
+      __syncthreads();
+      n_sort = min(sh.ngather, kSampleGatherCap);
+    } else {
+    // radix selection of the k-th key, four bits per pass
+    uint32_t pref = 0;
+    int krem = k;
+    int n_eq = 0;
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int shift = L::kBits - 4 * (pass + 1);
+      const uint32_t hi_mask = pass == 0 ? 0u : ((~0u << (shift + 4)) & (L::kBits == 16 ? 0xffffu : ~0u));
+      int cnt[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) cnt[j] = 0;
+      sweep([&](int id, uint32_t bits) {
+        const uint32_t key = L::key(bits);
+        if ((key & hi_mask) == pref) {
+          const int d = (key >> shift) & 15;
+          cnt[0] += 1;
+#pragma unroll
+          for (int q = 1; q < 16; ++q) cnt[q] += d >= q ? 1 : 0;
+        }
+      });
+      // block totals of the 16 counters
+#pragma unroll
+      for (int j = 0; j < 16; ++j) cnt[j] = wave_sum_i(cnt[j]);
+      if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sh.ired[pass & 1][wave][j] = cnt[j];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        int t = 0;
+#pragma unroll
+        for (int w = 0; w < kSampleWaves; ++w) t += sh.ired[pass & 1][w][j];
+        cnt[j] = t;
+      }
+      // forbidden ids count at the -inf key
+      for (int f = 0; f < nf; ++f) {
+        const uint32_t rk = sh.fkey[f];
+        if (rk == neg_key) continue;
+        if ((rk & hi_mask) == pref) {
+          const int d = (rk >> shift) & 15;
+#pragma unroll
+          for (int q = 0; q < 16; ++q) cnt[q] -= d >= q ? 1 : 0;
+        }
+        if ((neg_key & hi_mask) == pref) {
+          const int d = (neg_key >> shift) & 15;
+#pragma unroll
+          for (int q = 0; q < 16; ++q) cnt[q] += d >= q ? 1 : 0;
+        }
+      }
+      // largest digit whose ids (with this prefix) number at least krem
+      // (q = 0 always qualifies: cnt[0] >= krem by construction)
+      int dstar = 0, above = 0;
+      bool found = false;
+#pragma unroll
+      for (int q = 15; q >= 0; --q) {
+        const int c_next = q == 15 ? 0 : cnt[q + 1];
+        if (!found && cnt[q] >= krem) {
+          found = true;
+          dstar = q;
+          above = c_next;
+        }
+      }
+      krem -= above;
+      pref |= (uint32_t)dstar << shift;
+      n_eq = cnt[dstar] - above;  // ids whose key equals the prefix so far
+    }
+    // the candidates: every id whose key is at least the k-th key
     const uint32_t tkey = pref;
     const int need = krem;
     const int n_gt = k - need;
-    int gt_base = 0, eq_base = 0;
-    for (int t0 = 0; t0 < vocab; t0 += kSampleTile) {
-      const int i0 = t0 + tid * 8;
-      uint32_t key[8];
-      bool ok[8];
-      int ngt = 0, neq = 0;
-      if (i0 < vocab) {
-        uint32_t bits[8];
-        tile8(i0, bits, ok);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          uint32_t kk = L::key(bits[j]);
-          if (ok[j] && (kk >= tkey || tkey <= neg_key) && forbidden_id(i0 + j)) kk = neg_key;
-          key[j] = ok[j] ? kk : 0u;
-          ngt += (ok[j] && kk > tkey) ? 1 : 0;
-          neq += (ok[j] && kk == tkey) ? 1 : 0;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          ok[j] = false;
-          key[j] = 0u;
-        }
-      }
-      const int packed = ngt | (neq << 16);
-      const int incl = wave_incl_scan_i(packed, lane);
-      if (lane == 63) sh.iscan[wave] = incl;
+    const int n_ge = n_gt + n_eq;
+    if (n_ge <= kSampleGatherCap) {
+      // all of them, in no order (the sort below puts the lower of equal
+      // ids first and keeps the top k)
+      if (tid == 0) sh.ngather = 0;
       __syncthreads();
-      int wbase = 0, ttot = 0;
-#pragma unroll
-      for (int w = 0; w < kSampleWaves; ++w) {
-        wbase += w < wave ? sh.iscan[w] : 0;
-        ttot += sh.iscan[w];
-      }
-      __syncthreads();
-      const int excl = wbase + incl - packed;
-      int rg = gt_base + (excl & 0xffff);
-      int re = eq_base + (excl >> 16);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (!ok[j]) continue;
-        const unsigned long long ck =
-            ((unsigned long long)key[j] << 32) | (0xffffffffu - (uint32_t)(i0 + j));
-        if (key[j] > tkey) {
-          if (rg < n_gt) sh.cand[rg] = ck;
-          ++rg;
-        } else if (key[j] == tkey) {
-          if (re < need) sh.cand[n_gt + re] = ck;
-          ++re;
+      sweep([&](int id, uint32_t bits) {
+        uint32_t kk = L::key(bits);
+        if ((kk >= tkey || tkey <= neg_key) && nf > 0 && forbidden_id(id)) kk = neg_key;
+        if (kk >= tkey) {
+          const int slot = atomicAdd(&sh.ngather, 1);
+          if (slot < kSampleGatherCap)
+            sh.cand[slot] = ((unsigned long long)kk << 32) | (0xffffffffu - (uint32_t)id);
         }
-      }
-      gt_base += ttot & 0xffff;
-      eq_base += ttot >> 16;
-      if (gt_base >= n_gt && eq_base >= need) break;
-    }
-    // bitonic sort, descending, padded to a power of two
-    int kp = 1;
-    while (kp < k) kp <<= 1;
-    for (int i = k + tid; i < kp; i += kSampleThreads) sh.cand[i] = 0ull;
-    __syncthreads();
-    for (int size = 2; size <= kp; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int i = tid; i < (kp >> 1); i += kSampleThreads) {
-          const int pos = 2 * i - (i & (stride - 1));
-          const int oth = pos + stride;
-          const bool desc = (pos & size) == 0;
-          const unsigned long long p0 = sh.cand[pos], p1 = sh.cand[oth];
-          if (desc ? (p0 < p1) : (p0 > p1)) {
-            sh.cand[pos] = p1;
-            sh.cand[oth] = p0;
+      });
+      __syncthreads();
+      n_sort = min(sh.ngather, kSampleGatherCap);
+    } else {
+      // more ties at the k-th key than fit: take the lowest ids of them,
+      // walking the row in id order
+      int gt_base = 0, eq_base = 0;
+      for (int t0 = 0; t0 < vocab; t0 += kSampleTile) {
+        const int i0 = t0 + tid * 8;
+        uint32_t key[8];
+        bool ok[8];
+        int ngt = 0, neq = 0;
+        if (i0 < vocab) {
+          uint32_t bits[8];
+          tile8(i0, bits, ok);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            uint32_t kk = L::key(bits[j]);
+            if (ok[j] && (kk >= tkey || tkey <= neg_key) && forbidden_id(i0 + j)) kk = neg_key;
+            key[j] = ok[j] ? kk : 0u;
+            ngt += (ok[j] && kk > tkey) ? 1 : 0;
+            neq += (ok[j] && kk == tkey) ? 1 : 0;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            ok[j] = false;
+            key[j] = 0u;
           }
         }
+        const int packed = ngt | (neq << 16);
+        const int incl = wave_incl_scan_i(packed, lane);
+        if (lane == 63) sh.iscan[wave] = incl;
         __syncthreads();
+        int wbase = 0, ttot = 0;
+#pragma unroll
+        for (int w = 0; w < kSampleWaves; ++w) {
+          wbase += w < wave ? sh.iscan[w] : 0;
+          ttot += sh.iscan[w];
+        }
+        __syncthreads();
+        const int excl = wbase + incl - packed;
+        int rg = gt_base + (excl & 0xffff);
+        int re = eq_base + (excl >> 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (!ok[j]) continue;
+          const unsigned long long ck =
+              ((unsigned long long)key[j] << 32) | (0xffffffffu - (uint32_t)(i0 + j));
+          if (key[j] > tkey) {
+            if (rg < n_gt) sh.cand[rg] = ck;
+            ++rg;
+          } else if (key[j] == tkey) {
+            if (re < need) sh.cand[n_gt + re] = ck;
+            ++re;
+          }
+        }
+        gt_base += ttot & 0xffff;
+        eq_base += ttot >> 16;
+        if (gt_base >= n_gt && eq_base >= need) break;
       }
+      n_sort = k;
+    }
+    }
+    // Order the candidates by (value desc, id asc): composite keys are
+    // distinct, so an entry's position is the number of entries above it.
+    // Up to kSampleRankSort entries: every thread ranks its entries against
+    // all of them (broadcast LDS reads, one barrier); more: a bitonic sort.
+    if (n_sort <= kSampleRankSort) {
+      for (int i = tid; i < n_sort; i += kSampleThreads) {
+        const unsigned long long ci = sh.cand[i];
+        int r = 0;
+        for (int j = 0; j < n_sort; ++j) r += sh.cand[j] > ci ? 1 : 0;
+        if (r < k) sh.top[r] = ci;
+      }
+      __syncthreads();
+    } else {
+      int kp = 1;
+      while (kp < n_sort) kp <<= 1;
+      for (int i = n_sort + tid; i < kp; i += kSampleThreads) sh.cand[i] = 0ull;
+      __syncthreads();
+      for (int size = 2; size <= kp; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          for (int i = tid; i < (kp >> 1); i += kSampleThreads) {
+            const int pos = 2 * i - (i & (stride - 1));
+            const int oth = pos + stride;
+            const bool desc = (pos & size) == 0;
+            const unsigned long long p0 = sh.cand[pos], p1 = sh.cand[oth];
+            if (desc ? (p0 < p1) : (p0 > p1)) {
+              sh.cand[pos] = p1;
+              sh.cand[oth] = p0;
+            }
+          }
+          __syncthreads();
+        }
+      }
+      for (int i = tid; i < k; i += kSampleThreads) sh.top[i] = sh.cand[i];
+      __syncthreads();
     }
 
     // 4. softmax, top-p cut, inverse CDF (wavefront 0; lane l owns entries
@@ -531,7 +694,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
     if (wave == 0 && !a.greedy) {
       constexpr int kMaxE = kSampleMaxTopK / 64;
       const int E = (k + 63) / 64;
-      const float m = L::value((uint32_t)(sh.cand[0] >> 32)) / a.temperature;
+      const float m = L::value((uint32_t)(sh.top[0] >> 32)) / a.temperature;
       float e[kMaxE];
       float loc = 0.f;
 #pragma unroll
@@ -539,7 +702,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
         const int i = lane * E + j;
         e[j] = 0.f;
         if (j < E && i < k)
-          e[j] = expf(L::value((uint32_t)(sh.cand[i] >> 32)) / a.temperature - m);
+          e[j] = expf(L::value((uint32_t)(sh.top[i] >> 32)) / a.temperature - m);
         loc += e[j];
       }
       const float sum = wave_sum_f(loc);
@@ -581,7 +744,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
     }
     __syncthreads();
     const int pos = a.greedy ? 0 : sh.iscan[0];
-    chosen = (int)(0xffffffffu - (uint32_t)(sh.cand[pos] & 0xffffffffu));
+    chosen = (int)(0xffffffffu - (uint32_t)(sh.top[pos] & 0xffffffffu));
   }
   if (tid == 0) {
     a.token_out[row] = chosen;
