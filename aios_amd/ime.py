@@ -165,6 +165,15 @@ class CandidateGroupRuntime:
         self.ctx.page_table = self.page_table
         set_global_ctx(self.ctx)
 
+    @classmethod
+    def from_bundle(cls, path, device="cuda", **kw) -> "CandidateGroupRuntime":
+        """A runtime over an exported weight bundle (model.safetensors +
+        config.json, aios_amd.weights)."""
+        from aios_amd.weights import load_bundle
+
+        config, weights = load_bundle(path, device)
+        return cls(config, weights, device, **kw)
+
 
 class CandidateGroupEngine:
     """``use_graphs`` (default) replays each decode step from a HIP graph

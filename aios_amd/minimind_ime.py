@@ -127,7 +127,8 @@ class MiniMindBlockAttnResForCausalLM(Qwen3ForCausalLM):
             raise RuntimeError("AttnRes block produced no residual delta")
         if batch.is_prefill and not batch.return_all_logits:
             h = h[batch.attn_metadata.get_last_indices(batch.size)]
-        logits, _ = ops.add_rmsnorm_linear(h, None, self.w["final_norm"], eps, embed)
+        logits, _ = ops.add_rmsnorm_linear(h, None, self.w["final_norm"], eps,
+                                           self.w.get("lm_head", embed))
         return logits
 
 

@@ -60,6 +60,8 @@ def init_weights(config: ModelConfig, seed: int, device="cpu",
     if config.residual_type == "block_attnres":
         w["final_res_query"] = lin(1, h)[0]
         w["final_res_norm"] = torch.ones(h, device=dev, dtype=dtype)
+    if not config.tie_word_embeddings:
+        w["lm_head"] = lin(config.vocab_size, h)
     return w
 
 
@@ -144,5 +146,5 @@ class Qwen3ForCausalLM:
             last = batch.attn_metadata.get_last_indices(batch.size)
             h, residual = h[last], residual[last]
         logits, _ = ops.add_rmsnorm_linear(h, residual, self.w["final_norm"], c.rms_norm_eps,
-                                           self.w["embed"])
+                                           self.w.get("lm_head", self.w["embed"]))
         return logits

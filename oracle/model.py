@@ -109,7 +109,7 @@ class OracleModel:
             residual = x + residual
             h = self._mlp(lw, _rms(residual, lw["post_norm"], c.rms_norm_eps))
         x = _rms(h + residual, self.w["final_norm"], c.rms_norm_eps)
-        return x[:, start:] @ self.w["embed"].T
+        return x[:, start:] @ self.w.get("lm_head", self.w["embed"]).T
 
     def _attnres_logits(self, ids: torch.Tensor, start: int) -> torch.Tensor:
         """Block-AttnRes trunk (minimind_ime.py:193-326): a bank of the
@@ -133,7 +133,7 @@ class OracleModel:
                 bank.append(partial)
         h = self._mix(bank, self.w["final_res_query"], self.w["final_res_norm"])
         x = _rms(h, self.w["final_norm"], c.rms_norm_eps)
-        return x[:, start:] @ self.w["embed"].T
+        return x[:, start:] @ self.w.get("lm_head", self.w["embed"]).T
 
     @torch.no_grad()
     def candidates(self, prefix, n: int, steps: int):

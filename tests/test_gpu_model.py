@@ -446,3 +446,23 @@ def test_graph_replay_matches_eager_sampled():
         assert [x.average_logprob for x in g.raw_candidates] == \
             [x.average_logprob for x in e.raw_candidates]
     assert len(graphed._graphs) == 1
+
+
+def test_runtime_from_exported_bundle(tmp_path):
+    """A bundle written in the exporter's layout runs the same CandidateGroup
+    as the in-memory weights it was written from (Block-AttnRes trunk)."""
+    from aios_amd.weights import save_bundle
+
+    c = MINIMIND_ATTNRES_0P214B.with_layers(8)
+    w = init_weights(c, 12, "cpu")
+    save_bundle(c, w, tmp_path)
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=6)
+    prefix = _prefix(12, 64, c.vocab_size)
+    a = CandidateGroupEngine(CandidateGroupRuntime(c, weights_to(w, "cuda"), "cuda",
+                                                   num_pages=512)).complete(prefix, cfg)
+    reset_global_ctx()
+    b = CandidateGroupEngine(CandidateGroupRuntime.from_bundle(tmp_path, "cuda",
+                                                               num_pages=512)).complete(prefix, cfg)
+    assert [x.token_ids for x in a.raw_candidates] == [x.token_ids for x in b.raw_candidates]
+    assert [x.average_logprob for x in a.raw_candidates] == \
+        [x.average_logprob for x in b.raw_candidates]
