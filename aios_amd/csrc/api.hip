@@ -257,6 +257,8 @@ int aios_attn_prefill(const aios_attn_plan_t* p, const void* q, int64_t q_tok_st
   a.group = p->group;
   a.scale_log2 = sm_scale * aios::kLog2e;
   a.q_tile = p->prefill_q_tile;
+  a.q_tiles = p->num_q_tiles;
+  a.batch = p->batch_size;
   a.out = static_cast<aios::bf16*>(out);
   return check_hip(aios::launch_prefill(D, 4, a, p->num_q_tiles, p->batch_size,
                                         static_cast<hipStream_t>(stream)),

@@ -20,9 +20,17 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
   const int l16 = lane & 15;
   const int lg = lane >> 4;
   const int G = a.group;
-  const int qt = blockIdx.x;
-  const int h = blockIdx.y;
-  const int r = blockIdx.z;
+  // One flat grid: consecutive workgroups take consecutive kv-heads (the
+  // hardware deals workgroups round-robin to the XCDs, so with 8 kv-heads
+  // each XCD's L2 holds one head's K/V, read by all of that head's query
+  // tiles), and the query tiles run from the last (the longest causal KV
+  // range) to the first, so the short tiles fill in behind the long ones
+  // instead of the long ones forming the tail.
+  const int flat = blockIdx.x;
+  const int h = flat % a.num_kv_heads;
+  const int rest = flat / a.num_kv_heads;
+  const int r = rest % a.batch;
+  const int qt = a.q_tiles - 1 - rest / a.batch;
   const int q_start = a.cu_q[r];
   const int q_len = a.cu_q[r + 1] - q_start;
   if (qt * a.q_tile >= q_len) return;
@@ -76,7 +84,7 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
 hipError_t launch_prefill(int D, int NW, const PrefillArgs& a, int q_tiles, int batch,
                           hipStream_t s) {
   (void)NW;
-  const dim3 grid(q_tiles, a.num_kv_heads, batch);
+  const dim3 grid(q_tiles * a.num_kv_heads * batch);
   if (q_tiles == 0 || batch == 0) return hipSuccess;
   switch (D) {
     case 64: hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(kEngineThreads), 0, s, a); break;

@@ -81,7 +81,9 @@ struct PrefillArgs {
   int32_t num_kv_heads;
   int32_t group;
   float scale_log2;
-  int32_t q_tile;  // query tokens per workgroup
+  int32_t q_tile;   // query tokens per workgroup
+  int32_t q_tiles;  // query tiles of the longest request
+  int32_t batch;
   bf16* out;
 };
 
