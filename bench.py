@@ -392,10 +392,15 @@ def main() -> int:
     indices = wl.indices.to(dev)
     cu_k = wl.cu_k.to(dev)
     cu_q = torch.arange(n + 1, dtype=torch.int32)
-    t_plan = time.perf_counter()
-    plan = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=shape.prefix_len,
-                      prefix_chunk_len=args.chunk)
-    plan_us = (time.perf_counter() - t_plan) * 1e6
+    # host planning cost per batch: median of 20 calls after a first one
+    # (which also loads the library and queries the device)
+    plan_times = []
+    for _ in range(21):
+        t_plan = time.perf_counter()
+        plan = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=shape.prefix_len,
+                          prefix_chunk_len=args.chunk)
+        plan_times.append((time.perf_counter() - t_plan) * 1e6)
+    plan_us = sorted(plan_times[1:])[10]
     ws = torch.empty(max(plan.ws_bytes, 256), dtype=torch.uint8, device=dev)
     out = torch.empty(nl, n, hq, d, dtype=torch.bfloat16, device=dev)
     plan_casc = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=shape.prefix_len,
