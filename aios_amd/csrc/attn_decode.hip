@@ -74,8 +74,6 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
     const float l_tot = eng.l_run[rt];
     if (!ok[rt]) continue;
     const int m = rows[rt];
-    const int b = m / G;
-    const int g = m - b * G;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     // One store per accumulator tile: 16 rows x 16 dims, 512 contiguous bytes.
 #pragma unroll
