@@ -30,9 +30,10 @@ models).
 """
 from __future__ import annotations
 
+import math
 import threading
 import time
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import torch
 
@@ -83,14 +84,56 @@ class CandidateGroupConfig:
     seed: int = 20260814
     min_new_tokens: int = 0
     blocked_token_ids: tuple[int, ...] = ()  # with EOS: forbidden before min_new_tokens
+    # Adaptive refill (ime.py:333-370, 481-588): further sampled rounds while
+    # fewer than display_candidates valid distinct candidates exist, up to
+    # max_candidates attempts in all (0: no refill); defaults of
+    # ImeGenerationConfig (ime.py:36-53).
+    max_candidates: int = 0
+    refill_batch_size: int = 8
+    min_refill_batch_size: int = 2
+    refill_temperature: float = 0.75
+    refill_temperature_step: float = 0.10
+    max_refill_temperature: float = 0.95
+    refill_top_k: int = 96
+    refill_top_k_step: int = 32
+    max_refill_top_k: int = 160
+    refill_top_p: float = 0.95
+    refill_avoid_exact_repeats: bool = True
+    refill_ban_min_prefix_tokens: int = 2
+    refill_deadline_ms: float = 0.0  # no new round after this wall time (0: none)
 
     def validate(self) -> None:
         if self.num_candidates < self.display_candidates or self.display_candidates < 1:
             raise ValueError("num_candidates must cover display_candidates")
         if self.max_new_tokens < 1:
             raise ValueError("max_new_tokens must be positive")
-        if self.min_new_tokens < 0:
-            raise ValueError("min_new_tokens must be non-negative")
+        if not 0 <= self.min_new_tokens <= self.max_new_tokens:
+            raise ValueError("min_new_tokens must be within max_new_tokens")
+        if self.max_candidates:  # refill rules (ime.py:58-96)
+            if self.max_candidates < self.num_candidates:
+                raise ValueError("max_sampling_attempts must cover the initial attempts")
+            if self.refill_batch_size < 1:
+                raise ValueError("refill_batch_size must be positive")
+            if not 1 <= self.min_refill_batch_size <= self.refill_batch_size:
+                raise ValueError("min_refill_batch_size must be within refill_batch_size")
+            if not 0.0 < self.refill_top_p <= 1.0:
+                raise ValueError("refill_top_p must be in (0, 1]")
+            if self.refill_temperature <= 0.0:
+                raise ValueError("IME candidate sampling temperatures must be positive")
+            if self.refill_temperature_step < 0.0:
+                raise ValueError("refill_temperature_step must be non-negative")
+            if self.max_refill_temperature < self.refill_temperature:
+                raise ValueError("max_refill_temperature must cover refill_temperature")
+            if self.refill_top_k < 1:
+                raise ValueError("IME candidate top_k values must be positive")
+            if self.refill_top_k_step < 0:
+                raise ValueError("refill_top_k_step must be non-negative")
+            if self.max_refill_top_k < self.refill_top_k:
+                raise ValueError("max_refill_top_k must cover refill_top_k")
+            if self.refill_deadline_ms < 0.0:
+                raise ValueError("refill_deadline_ms must be non-negative")
+            if self.refill_ban_min_prefix_tokens < 1:
+                raise ValueError("refill_ban_min_prefix_tokens must be positive")
 
     def blocked_ids(self) -> tuple[int, ...]:
         """ime.py:948-955: terminal ids and EOS, blocked before min_new_tokens."""
@@ -98,6 +141,31 @@ class CandidateGroupConfig:
         if self.eos_token_id is not None:
             ids.add(int(self.eos_token_id))
         return tuple(sorted(ids))
+
+
+def candidate_valid(c: "Candidate", config: CandidateGroupConfig) -> bool:
+    """Without a tokenizer the text filters of ime.py:187-370 reduce to: at
+    least max(1, min_new_tokens) tokens and not cut off by cancellation."""
+    return len(c.token_ids) >= max(1, config.min_new_tokens) and c.stop_reason != "cancelled"
+
+
+def adaptive_refill_attempts(candidates, config: CandidateGroupConfig, attempts_used: int) -> int:
+    """Branches for the next refill round (ime.py:333-370): enough to fill
+    the Top-k deficit at the observed valid-distinct yield, at least
+    min_refill_batch_size and twice the deficit, at most the round cap and
+    the remaining budget."""
+    remaining = config.max_candidates - attempts_used
+    if remaining <= 0:
+        return 0
+    unique = {c.token_ids for c in candidates if candidate_valid(c, config)}
+    deficit = config.display_candidates - len(unique)
+    if deficit <= 0:
+        return 0
+    floor = 1.0 / max(1, config.refill_batch_size)
+    observed = len(unique) / len(candidates) if candidates else floor
+    predicted = math.ceil(deficit / max(floor, observed))
+    planned = max(config.min_refill_batch_size, deficit * 2, predicted)
+    return min(planned, config.refill_batch_size, remaining)
 
 
 @dataclass(frozen=True)
@@ -120,6 +188,7 @@ class CompletionResult:
     unique_kv_pages: int
     cancelled: bool
     prefix_logits: torch.Tensor | None = field(default=None, repr=False)
+    refill_rounds: int = 0
 
 
 def select_top(candidates, k: int) -> tuple[Candidate, ...]:
@@ -234,7 +303,9 @@ class CandidateGroupEngine:
         max_total = p + config.max_new_tokens
         if max_total > min(self.rt.config.max_position_embeddings, self.rt.max_context):
             raise ValueError("prefix + output exceeds context limit")
-        required = p + n * max(0, config.max_new_tokens - 1)
+        rows = max(n, min(config.refill_batch_size, self.rt.max_attempts)
+                   if config.max_candidates > n else 0)
+        required = p + rows * max(0, config.max_new_tokens - 1)
         if required > self.rt.num_pages:
             raise ValueError(
                 f"CandidateGroup KV budget is too small: need up to {required} pages, "
@@ -254,10 +325,50 @@ class CandidateGroupEngine:
             if allocated:
                 self.rt.cache_manager._free(torch.cat(allocated))
                 allocated = []
+            # Adaptive refill rounds (ime.py:504-588): the round's branch KV
+            # is freed before the next round is planned.
+            rounds, used = 0, n
+            while not cancelled and config.max_candidates > used:
+                if config.refill_deadline_ms > 0.0 and \
+                        (time.perf_counter() - wall) * 1e3 >= config.refill_deadline_ms:
+                    break
+                attempts = min(adaptive_refill_attempts(raw, config, used), self.rt.max_attempts)
+                if attempts == 0:
+                    break
+                rounds += 1
+                sp = SamplingParams(
+                    temperature=min(config.max_refill_temperature, config.refill_temperature
+                                    + (rounds - 1) * config.refill_temperature_step),
+                    top_k=min(config.max_refill_top_k,
+                              config.refill_top_k + (rounds - 1) * config.refill_top_k_step),
+                    top_p=config.refill_top_p)
+                banned = []
+                if config.refill_avoid_exact_repeats:
+                    seen = set()
+                    for c in sorted(raw, key=lambda c: c.average_logprob, reverse=True):
+                        if not candidate_valid(c, config) or c.token_ids in seen:
+                            continue
+                        if len(c.token_ids) > config.refill_ban_min_prefix_tokens:
+                            banned.append(c.token_ids)
+                            seen.add(c.token_ids)
+                round_cfg = replace(config, num_candidates=attempts, sampling=sp,
+                                    seed=config.seed + used * 100_003)
+                r_raw, r_alloc, r_gen, r_act, r_cancel = self._generate(
+                    prefix_logits, page_table, p, round_cfg, cancellation, banned=banned)
+                unique_pages = max(unique_pages, len(prefix_pages) + sum(len(a) for a in r_alloc))
+                if r_alloc:
+                    self.rt.cache_manager._free(torch.cat(r_alloc))
+                raw += r_raw
+                used += attempts
+                generated += r_gen
+                active_tokens += r_act
+                cancelled |= r_cancel
             ended.record()
             ended.synchronize()
             return CompletionResult(
-                candidates=select_top(raw, config.display_candidates),
+                candidates=select_top([c for c in raw if candidate_valid(c, config)]
+                                      if config.max_candidates else raw,
+                                      config.display_candidates),
                 raw_candidates=tuple(raw),
                 prefix_tokens=p,
                 reused_prefix_tokens=reused,
@@ -268,6 +379,7 @@ class CandidateGroupEngine:
                 unique_kv_pages=unique_pages,
                 cancelled=cancelled,
                 prefix_logits=prefix_logits,
+                refill_rounds=rounds,
             )
         finally:
             if allocated:
@@ -334,7 +446,13 @@ class CandidateGroupEngine:
             logits = self.rt.model.forward()
         return logits, pages
 
-    def _generate(self, prefix_logits, page_table, prefix_len: int, config, cancellation):
+    def _generate(self, prefix_logits, page_table, prefix_len: int, config, cancellation,
+                  banned=()):
+        """One round of n candidates (ime.py:891-1054).  ``banned``: token
+        sequences a row may not reproduce -- once its output so far equals a
+        banned sequence's first ``step`` tokens (step >= the ban's minimum
+        prefix), that sequence's next token is forbidden for it
+        (ime.py:977-1004)."""
         n = config.num_candidates
         dev = self.rt.device
         t_max = config.max_new_tokens
@@ -349,10 +467,24 @@ class CandidateGroupEngine:
             blocked_t = (torch.tensor(blocked, dtype=torch.int32, device=dev) if blocked
                          else None)
 
+            ban_len = max((len(b) for b in banned), default=0)
+            ban_ids = ban_lens = None
+            if banned:
+                ban_ids = torch.full((len(banned), ban_len), -1, dtype=torch.long, device=dev)
+                for i, b in enumerate(banned):
+                    ban_ids[i, : len(b)] = torch.tensor(b, dtype=torch.long, device=dev)
+                ban_lens = torch.tensor([len(b) for b in banned], dtype=torch.long, device=dev)
+
             def pick(logits, rows, step):
                 col = torch.full((1,), step, dtype=torch.int64, device=dev)
+                by_row = None
+                if banned and config.refill_ban_min_prefix_tokens <= step < ban_len:
+                    match = (out_ids[rows, :step][:, None, :] == ban_ids[None, :, :step]).all(-1)
+                    match &= ban_lens[None, :] > step
+                    nxt = ban_ids[None, :, step].expand(len(rows), -1)
+                    by_row = torch.where(match, nxt, torch.full_like(nxt, -1)).contiguous()
                 return sample_step(logits, config.sampling, uni[rows], col, blocked_t,
-                                   config.min_new_tokens)
+                                   config.min_new_tokens, forbidden_by_row=by_row)
 
             # every candidate draws its first token from the prefix logits
             token, raw_lp = pick(prefix_logits[:1].expand(n, -1), torch.arange(n, device=dev), 0)

@@ -74,6 +74,10 @@ def sample_step(logits: torch.Tensor, params: SamplingParams, uniforms: torch.Te
         raise ValueError("uniforms must be float32 [rows, steps] with contiguous rows")
     if step.dtype != torch.int64 or step.numel() != 1:
         raise ValueError("step must be a one-element int64 tensor")
+    if forbidden_by_row is not None and (
+            forbidden_by_row.dtype != torch.int64 or forbidden_by_row.ndim != 2
+            or forbidden_by_row.shape[0] != rows or not forbidden_by_row.is_contiguous()):
+        raise ValueError("forbidden_by_row must be contiguous int64 [rows, n]")
     tok, lp = out if out is not None else (
         torch.empty(rows, dtype=torch.int64, device=logits.device),
         torch.empty(rows, dtype=torch.float32, device=logits.device))

@@ -466,3 +466,53 @@ def test_runtime_from_exported_bundle(tmp_path):
     assert [x.token_ids for x in a.raw_candidates] == [x.token_ids for x in b.raw_candidates]
     assert [x.average_logprob for x in a.raw_candidates] == \
         [x.average_logprob for x in b.raw_candidates]
+
+
+def test_candidate_group_adaptive_refill():
+    """Refill rounds (ime.py:478-600, 333-370).  A greedy first round
+    (top_k 1) yields one distinct candidate, so one refill round of 8
+    branches follows at the refill schedule (temperature 0.75, top_k 96,
+    top_p 0.95, seeds seed + 8 * 100003 + i) with the first round's
+    sequence banned from step 2 on; every refill token is the sampling
+    oracle's draw from the GPU's logits with that row's ban applied."""
+    c = MINIMIND_0P1B.with_layers(4)
+    eng, _ = _engine(c, 31)
+    prefix = _prefix(31, 24, c.vocab_size)
+    rec = _record_decode_logits(eng)
+    t = 8
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=t, min_new_tokens=2,
+                               sampling=SamplingParams(temperature=0.35, top_k=1, top_p=1.0),
+                               max_candidates=24)
+    res = eng.complete(prefix, cfg)
+    raw = res.raw_candidates
+    assert res.refill_rounds >= 1 and len(raw) == 8 + 8 * res.refill_rounds
+    greedy = raw[0].token_ids
+    assert all(r.token_ids == greedy for r in raw[:8]) and len(greedy) == t
+    # round 2 against the oracle, with the ban
+    sp = SamplingParams(temperature=0.75, top_k=96, top_p=0.95)
+    uni = osamp.stateless_uniforms([cfg.seed + 8 * 100_003 + i for i in range(8)], t)
+    steps = [(list(range(8)), res.prefix_logits.float().cpu().expand(8, -1))] + rec[t - 1: 2 * (t - 1)]
+    checked = 0
+    for j, (rows, lg) in enumerate(steps):
+        assert rows == list(range(8))
+        for r in rows:
+            hist = raw[8 + r].token_ids
+            fb = [greedy[j]] if j >= 2 and hist[:j] == greedy[:j] else []
+            want, _, d = osamp.sample_row(lg[r].numpy(), sp.temperature, sp.top_k, sp.top_p,
+                                          float(uni[r, j]), fb, detail=True)
+            assert hist[j] not in fb
+            if d["u_margin"] > 1e-5 and d["cut_margin"] > 1e-5:
+                assert hist[j] == want, (j, r, hist[j], want)
+                checked += 1
+            else:
+                assert hist[j] in set(d["order"].tolist())
+    assert checked >= 0.9 * 8 * t
+    assert all(r.token_ids != greedy for r in raw[8:16])
+    shown = [x.token_ids for x in res.candidates]
+    assert len(shown) == 3 and len(set(shown)) == 3
+    eng.reset_prefix_cache()
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages
+    # deterministic: the same request reproduces every round
+    eng._decode_step = eng.__class__._decode_step.__get__(eng)
+    again = eng.complete(prefix, cfg)
+    assert [x.token_ids for x in again.raw_candidates] == [x.token_ids for x in raw]

@@ -6,7 +6,8 @@ import pytest
 import torch
 
 from aios_amd.core import Req, SamplingParams
-from aios_amd.ime import Candidate, CandidateGroupConfig, select_top, token_longest_common_prefix
+from aios_amd.ime import (Candidate, CandidateGroupConfig, adaptive_refill_attempts,
+                           candidate_valid, select_top, token_longest_common_prefix)
 from aios_amd.scheduler import CacheManager
 from oracle import prefix as oprefix
 
@@ -68,3 +69,54 @@ def test_req_lengths_follow_reference():
     assert (r.device_len, r.extend_len, r.remain_len) == (7, 3, 2)
     r.complete_one()
     assert (r.cached_len, r.device_len, r.extend_len, r.remain_len) == (7, 8, 1, 1)
+
+
+def _cands(seqs):
+    return [Candidate(tuple(s), -1.0, "max_new_tokens") for s in seqs]
+
+
+@pytest.mark.parametrize("seqs,used,want", [
+    # 8 branches, 1 distinct: deficit 2, yield floor 1/8 -> ceil(2/0.125)=16, cap 8
+    ([[1, 2, 3]] * 8, 8, 8),
+    # 8 branches, 2 distinct: deficit 1, yield 1/4 -> 4 = max(2, 2, 4)
+    ([[1, 2, 3]] * 7 + [[4, 5, 6]], 8, 4),
+    # 2 of 2 distinct: deficit 1, yield 1 -> max(min batch 2, 2*1, 1) = 2
+    ([[1, 2, 3], [4, 5, 6]], 8, 2),
+    # filled: no refill
+    ([[1, 1], [2, 2], [3, 3]], 8, 0),
+    # budget: 22 of 24 used -> at most 2
+    ([[1, 2, 3]] * 8, 22, 2),
+    ([[1, 2, 3]] * 8, 24, 0),
+    # empty candidates are invalid (min_new_tokens 2: one-token rows too)
+    ([[], [7], [1, 2]], 8, 6),  # 1 valid of 3: ceil(2 / (1/3)) = 6
+])
+def test_adaptive_refill_attempts(seqs, used, want):
+    """ime.py:333-370 worked by hand for display 3, budget 24, round cap 8."""
+    cfg = CandidateGroupConfig(num_candidates=8, max_candidates=24, min_new_tokens=2)
+    assert adaptive_refill_attempts(_cands(seqs), cfg, used) == want
+
+
+def test_candidate_validity():
+    cfg = CandidateGroupConfig(min_new_tokens=2)
+    assert candidate_valid(Candidate((1, 2), -1.0, "eos"), cfg)
+    assert not candidate_valid(Candidate((1,), -1.0, "eos"), cfg)
+    assert not candidate_valid(Candidate((1, 2), -1.0, "cancelled"), cfg)
+    assert not candidate_valid(Candidate((), -1.0, "eos"), CandidateGroupConfig())
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(max_candidates=4), "must cover the initial attempts"),
+    (dict(max_candidates=24, refill_batch_size=0), "refill_batch_size must be positive"),
+    (dict(max_candidates=24, min_refill_batch_size=9), "min_refill_batch_size"),
+    (dict(max_candidates=24, refill_top_p=0.0), "refill_top_p"),
+    (dict(max_candidates=24, refill_temperature=0.0), "temperatures must be positive"),
+    (dict(max_candidates=24, max_refill_temperature=0.5), "max_refill_temperature"),
+    (dict(max_candidates=24, refill_top_k=0), "top_k values must be positive"),
+    (dict(max_candidates=24, max_refill_top_k=64), "max_refill_top_k"),
+    (dict(max_candidates=24, refill_deadline_ms=-1.0), "refill_deadline_ms"),
+    (dict(max_candidates=24, refill_ban_min_prefix_tokens=0), "refill_ban_min_prefix_tokens"),
+    (dict(min_new_tokens=20), "min_new_tokens must be within max_new_tokens"),
+])
+def test_refill_config_validation(kw, msg):
+    with pytest.raises(ValueError, match=msg):
+        CandidateGroupConfig(num_candidates=8, **kw).validate()
