@@ -17,11 +17,14 @@ full-model CandidateGroup Top-3 latency of the MiniMind-0.1B-shaped model
 (``candidate_group``: p50/p95 over 30 seeded prefixes after 5 warmups, with
 graph-replayed and eager decode steps; ``candidate_group_sampled``: the same
 model with the reference's default sampled candidates, temperature 0.35,
-top_k 50, top_p 0.9, 12 tokens) and of the Qwen3-0.6B-shaped model
+top_k 50, top_p 0.9, 12 tokens, refill up to 12 candidates;
+``candidate_group_refill``: a greedy first round that forces one refill
+round of 8) and of the Qwen3-0.6B-shaped model
 on a 128-token prefix extended by 2 ids (``candidate_group_qwen3_0p6b``:
 the cross-keystroke case, 8 candidates x 24 steps) and of the 0.214B
 Block-AttnRes-shaped model (``candidate_group_attnres_0p214b``: 64-token
-prefix, 8 candidates x 32 steps, 65 depth mixers per forward), the 65-mixer
+prefix, sampled rounds of 8 candidates x 32 steps up to 24 candidates, 65
+depth mixers per forward), the 65-mixer
 depth-routing pipeline alone (``attnres_pipeline``), the reference's CPU attention
 path (restated, oracle/sdpa_cpu.py) timed on a bounded sample on the host
 cores, and the causal prefill of the 4096-token prefix (``prefill``: one
@@ -173,7 +176,8 @@ def prefix_prefill(seed: int, reps: int = 10) -> dict:
 
 def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int = 32,
                     steps: int = 16, extend: int = 0, runs: int = 30, warmups: int = 5,
-                    sampling: tuple | None = None, min_new_tokens: int = 0) -> dict:
+                    sampling: tuple | None = None, min_new_tokens: int = 0,
+                    max_candidates: int = 0) -> dict:
     """Full CandidateGroup Top-3 latency of a synthetic-weight model.
 
     Default: the MiniMind-0.1B-shaped model (14 layers, hidden 768, 8q/2kv
@@ -189,7 +193,9 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int 
     decode-step graph); each run starts from an empty prefix cache.  With
     ``sampling`` = (temperature, top_k, top_p) the candidates are sampled
     with stateless uniforms (the reference's candidate rule) instead of
-    greedy from the top first tokens.
+    greedy from the top first tokens.  With ``max_candidates`` > 8, adaptive
+    refill rounds (eager steps) follow while fewer than 3 valid distinct
+    candidates exist, up to that many candidates in all.
     """
     import statistics
 
@@ -205,7 +211,7 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int 
     sp = None if sampling is None else SamplingParams(temperature=sampling[0], top_k=sampling[1],
                                                       top_p=sampling[2])
     cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=steps, sampling=sp, seed=seed,
-                               min_new_tokens=min_new_tokens)
+                               min_new_tokens=min_new_tokens, max_candidates=max_candidates)
     out = {"model": f"{model}-shaped ({c.num_layers}L, {c.hidden_size}, "
                     f"{c.num_qo_heads}q/{c.num_kv_heads}kv x {c.head_dim}, "
                     f"ffn {c.intermediate_size}, vocab {c.vocab_size})",
@@ -214,10 +220,11 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int 
            "candidates_rule": ("greedy from the top first tokens" if sp is None else
                                f"sampled: temperature {sp.temperature}, top_k {sp.top_k}, "
                                f"top_p {sp.top_p}, stateless uniforms, min_new_tokens "
-                               f"{min_new_tokens}")}
+                               f"{min_new_tokens}"),
+           "max_candidates": max_candidates or 8}
     for mode in ("graph", "eager"):
         eng = CandidateGroupEngine(rt, use_graphs=mode == "graph")
-        lat, gpu, gen = [], [], 0
+        lat, gpu, gen, rounds = [], [], 0, 0
         first = None
         for i in range(warmups + runs):
             g = torch.Generator().manual_seed(seed + 1000 + i)
@@ -234,6 +241,7 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int 
                 lat.append(dt)
                 gpu.append(r.gpu_latency_ms)
                 gen += r.generated_tokens
+                rounds += r.refill_rounds
         eng.reset_prefix_cache()
         lat.sort()
         p50 = statistics.median(lat)
@@ -241,7 +249,8 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int 
                      "top3_p95_ms": round(lat[max(0, int(round(0.95 * len(lat))) - 1)], 3),
                      "gpu_event_p50_ms": round(statistics.median(gpu), 3),
                      "first_call_ms": round(first, 3),
-                     "candidate_tokens_per_s": round(gen / (sum(lat) * 1e-3), 1)}
+                     "candidate_tokens_per_s": round(gen / (sum(lat) * 1e-3), 1),
+                     "refill_rounds_per_run": round(rounds / runs, 3)}
     del rt
     reset_global_ctx()
     torch.cuda.empty_cache()
@@ -553,7 +562,7 @@ def main() -> int:
         # Qwen3-0.6B-shaped: 128-token prefix extended by 2 ids (cross-keystroke
         # reuse), 8 candidates x 24 steps.
         result["candidate_group_sampled"] = candidate_group(
-            args.seed, steps=12, sampling=(0.35, 50, 0.9), min_new_tokens=2)
+            args.seed, steps=12, sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=12)
         _log(f"candidate group sampled {result['candidate_group_sampled']['graph']['top3_p50_ms']} "
              "ms p50")
         result["candidate_group_qwen3_0p6b"] = candidate_group(
@@ -561,9 +570,16 @@ def main() -> int:
             warmups=3)
         _log(f"candidate group qwen3-0.6b "
              f"{result['candidate_group_qwen3_0p6b']['graph']['top3_p50_ms']} ms p50")
+        # Refill exercised: a greedy first round (top_k 1) yields one distinct
+        # candidate, so every run adds a refill round of 8 sampled branches.
+        result["candidate_group_refill"] = candidate_group(
+            args.seed, steps=12, sampling=(0.35, 1, 1.0), min_new_tokens=2, max_candidates=24,
+            runs=10, warmups=2)
+        _log(f"candidate group refill {result['candidate_group_refill']['graph']['top3_p50_ms']} "
+             "ms p50")
         result["candidate_group_attnres_0p214b"] = candidate_group(
             args.seed, model="minimind-attnres-0.214b", prefix_tokens=64, steps=32, runs=20,
-            warmups=3)
+            warmups=3, sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=24)
         _log(f"candidate group attnres-0.214b "
              f"{result['candidate_group_attnres_0p214b']['graph']['top3_p50_ms']} ms p50")
     if not args.no_cpu_baseline:
