@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "aios_build_indices",
     "aios_rmsnorm",
     "aios_qk_norm_rope",
+    "aios_cg_step_begin",
+    "aios_cg_step_end",
     "aios_silu_mul",
     "aios_linear_rows",
     "aios_linear_rows_ex",
@@ -124,6 +126,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.aios_build_indices.argtypes = [_vp, _i64, _vp, _vp, _i32, _i32, _vp, _vp]
     lib.aios_rmsnorm.restype = ctypes.c_int
     lib.aios_rmsnorm.argtypes = [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i32, _f32, _vp]
+    lib.aios_cg_step_begin.restype = ctypes.c_int
+    lib.aios_cg_step_begin.argtypes = [_vp, _vp, _i32, _i32, _vp, _vp, _i64, _i32, _vp, _vp]
+    lib.aios_cg_step_end.restype = ctypes.c_int
+    lib.aios_cg_step_end.argtypes = [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _vp,
+                                     _vp, _vp, _vp, _vp, _vp]
     lib.aios_qk_norm_rope.restype = ctypes.c_int
     lib.aios_qk_norm_rope.argtypes = [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64,
                                       _vp, _vp, _vp, _f32, _vp]

@@ -519,6 +519,54 @@ int aios_linear_rows_ex(const void* x, int64_t x_stride, const void* weight, int
                    "linear_rows launch");
 }
 
+int aios_cg_step_begin(int64_t* step, const int32_t* pages, int32_t page_rows, int32_t rows,
+                       int32_t* out_loc, int32_t* page_table, int64_t pt_stride, int32_t pt_cols,
+                       int32_t* pos, void* stream) {
+  if (rows <= 0 || page_rows <= 0 || pt_cols <= 0 || pt_stride < pt_cols)
+    return fail(AIOS_ERR_INVALID, "cg_step_begin: bad sizes");
+  if (!step || !pages || !out_loc || !page_table || !pos)
+    return fail(AIOS_ERR_INVALID, "cg_step_begin: null pointer");
+  aios::CgStepArgs a = {};
+  a.rows = rows;
+  a.step = step;
+  a.pages = pages;
+  a.page_rows = page_rows;
+  a.out_loc = out_loc;
+  a.page_table = page_table;
+  a.pt_stride = pt_stride;
+  a.pt_cols = pt_cols;
+  a.pos = pos;
+  return check_hip(aios::cg_step_begin(a, static_cast<hipStream_t>(stream)), "cg_step_begin launch");
+}
+
+int aios_cg_step_end(int64_t* step, int32_t rows, const int64_t* tok, const float* raw, int64_t eos,
+                     uint8_t* finished, uint8_t* eos_hit, int64_t* out_ids, int64_t out_stride,
+                     int32_t out_cols, float* logp_sum, int64_t* counts, int64_t* tokens,
+                     int32_t* pos, int64_t* fed, void* stream) {
+  if (rows <= 0 || out_cols <= 0 || out_stride < out_cols)
+    return fail(AIOS_ERR_INVALID, "cg_step_end: bad sizes");
+  if (!step || !tok || !raw || !finished || !eos_hit || !out_ids || !logp_sum || !counts ||
+      !tokens || !pos || !fed)
+    return fail(AIOS_ERR_INVALID, "cg_step_end: null pointer");
+  aios::CgStepArgs a = {};
+  a.rows = rows;
+  a.step = step;
+  a.tok = tok;
+  a.raw = raw;
+  a.eos = eos < 0 ? -1 : eos;
+  a.finished = finished;
+  a.eos_hit = eos_hit;
+  a.out_ids = out_ids;
+  a.out_stride = out_stride;
+  a.out_cols = out_cols;
+  a.logp_sum = logp_sum;
+  a.counts = counts;
+  a.tokens = tokens;
+  a.pos = pos;
+  a.fed = fed;
+  return check_hip(aios::cg_step_end(a, static_cast<hipStream_t>(stream)), "cg_step_end launch");
+}
+
 int aios_greedy_select(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
                        int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                        void* stream) {

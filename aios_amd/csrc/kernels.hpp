@@ -129,6 +129,32 @@ struct LinearArgs {
   bf16* residual_out;    // prologue 1: bf16(x + residual) (may be null)
   int64_t ro_stride;
 };
+// Device state of a captured CandidateGroup decode step.
+struct CgStepArgs {
+  int32_t rows;
+  int64_t* step;            // [1] step index (device)
+  const int32_t* pages;     // [page_rows][rows] page of each row per step
+  int32_t page_rows;
+  int32_t* out_loc;         // [rows]
+  int32_t* page_table;      // [rows][pt_stride]
+  int64_t pt_stride;
+  int32_t pt_cols;
+  int32_t* pos;             // [rows]
+  const int64_t* tok;       // [rows] the step's pick
+  const float* raw;         // [rows] its raw log-prob
+  int64_t eos;              // -1: none
+  uint8_t* finished;        // [rows] bool
+  uint8_t* eos_hit;         // [rows] bool
+  int64_t* out_ids;         // [rows][out_stride]
+  int64_t out_stride;
+  int32_t out_cols;
+  float* logp_sum;          // [rows]
+  int64_t* counts;          // [rows]
+  int64_t* tokens;          // [rows] next input ids
+  int64_t* fed;             // [1] live rows fed so far
+};
+hipError_t cg_step_begin(const CgStepArgs& a, hipStream_t stream);
+hipError_t cg_step_end(const CgStepArgs& a, hipStream_t stream);
 bool skinny_gemm_supported(int64_t M, int64_t N, int64_t K);
 bool skinny_gemm_norm_supported(int64_t M, int64_t K);
 hipError_t skinny_gemm(const LinearArgs& a, int prologue, int epilogue, hipStream_t stream);

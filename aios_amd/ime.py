@@ -37,6 +37,7 @@ from dataclasses import dataclass, field, replace
 
 import torch
 
+from aios_amd import _lib
 from aios_amd.config import ModelConfig
 from aios_amd.core import Batch, Context, Req, SamplingParams, reset_global_ctx, set_global_ctx
 from aios_amd.sample import sample_step, stateless_uniforms
@@ -620,6 +621,9 @@ class _DecodeGraph:
         self.eos_hit = torch.zeros(rows, dtype=torch.bool, device=dev)
         self.fed = torch.zeros(1, dtype=torch.long, device=dev)
         self.row_ids = torch.arange(rows, dtype=torch.long, device=dev)
+        self.out_loc = torch.zeros(rows, dtype=torch.int32, device=dev)
+        self.tok = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.raw = torch.zeros(rows, dtype=torch.float32, device=dev)
         self.md = rt.model.attn_backend.prepare_static_decode(self.row_ids, kv_cap, plan_prefix,
                                                               rt.page_table)
         reqs = [Req(input_ids=torch.empty(1), cached_len=0, output_len=1, uid=r,
@@ -659,32 +663,33 @@ class _DecodeGraph:
         self.step.zero_()
 
     def _body(self) -> None:
+        """One step: the page-table column (aios_cg_step_begin), metadata
+        refresh, model, pick, then the state update (aios_cg_step_end) --
+        the ime.py:1010-1054 bookkeeping in two launches."""
         rt = self.rt
-        out_loc = self.pages.index_select(0, self.step).view(-1)
-        rt.page_table.index_put_((self.row_ids, self.pos.long()), out_loc)
+        lib = _lib.lib()
+        pt = rt.page_table
+        stream = torch.cuda.current_stream(self.rt.device).cuda_stream
+        _lib.check(lib.aios_cg_step_begin(
+            self.step.data_ptr(), self.pages.data_ptr(), self.pages.shape[0], self.rows,
+            self.out_loc.data_ptr(), pt.data_ptr(), pt.stride(0), pt.shape[1],
+            self.pos.data_ptr(), stream), "aios_cg_step_begin")
         self.md.refresh(self.pos[:1] + 1)
-        self.batch.out_loc = out_loc
+        self.batch.out_loc = self.out_loc
         with rt.ctx.forward_batch(self.batch):
             logits = rt.model.forward()
         if self.sampling is not None:
             tok, raw = sample_step(logits, self.sampling, self.uni, self.step + 1, self.blocked,
-                                   self.min_new)
+                                   self.min_new, out=(self.tok, self.raw))
         else:
-            tok, raw = greedy_select(logits)
-        live = ~self.finished
-        self.fed += live.sum()
-        emitted = live if self.eos is None else live & tok.ne(self.eos)
-        self.out_ids.index_copy_(1, self.step + 1,
-                                 torch.where(emitted, tok, torch.full_like(tok, -1))[:, None])
-        self.logp_sum += torch.where(emitted, raw, torch.zeros_like(raw))
-        self.counts += emitted.long()
-        if self.eos is not None:
-            hit = live & tok.eq(self.eos)
-            self.eos_hit |= hit
-            self.finished |= hit
-        self.tokens.copy_(tok)
-        self.pos += 1
-        self.step += 1
+            tok, raw = greedy_select(logits, out=(self.tok, self.raw))
+        _lib.check(lib.aios_cg_step_end(
+            self.step.data_ptr(), self.rows, tok.data_ptr(), raw.data_ptr(),
+            -1 if self.eos is None else int(self.eos), self.finished.data_ptr(),
+            self.eos_hit.data_ptr(), self.out_ids.data_ptr(), self.out_ids.stride(0),
+            self.out_ids.shape[1], self.logp_sum.data_ptr(), self.counts.data_ptr(),
+            self.tokens.data_ptr(), self.pos.data_ptr(), self.fed.data_ptr(), stream),
+            "aios_cg_step_end")
 
     def run_step(self) -> None:
         if self.graph is not None:

@@ -187,16 +187,25 @@ def build_indices(page_table: torch.Tensor, row_ids: torch.Tensor, cu_k: torch.T
     return out
 
 
-def greedy_select(logits: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+def greedy_select(logits: torch.Tensor,
+                  out: tuple[torch.Tensor, torch.Tensor] | None = None
+                  ) -> tuple[torch.Tensor, torch.Tensor]:
     """Greedy token per row and its raw log-probability (aios_greedy_select):
-    (argmax(logits, -1) as int64, log_softmax(logits.float())[token] as fp32)."""
+    (argmax(logits, -1) as int64, log_softmax(logits.float())[token] as fp32),
+    written into ``out`` (int64 [rows], fp32 [rows]) when given."""
     if logits.ndim != 2 or logits.stride(1) != 1 or not logits.is_cuda:
         raise ValueError("logits must be a 2-D GPU tensor with contiguous rows")
     if logits.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("logits must be bfloat16 or float32")
     rows, vocab = logits.shape
-    tok = torch.empty(rows, dtype=torch.int64, device=logits.device)
-    lp = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    if out is not None:
+        tok, lp = out
+        if (tok.dtype != torch.int64 or lp.dtype != torch.float32 or tok.numel() != rows
+                or lp.numel() != rows or not tok.is_contiguous() or not lp.is_contiguous()):
+            raise ValueError("out must be (int64 [rows], float32 [rows]) contiguous tensors")
+    else:
+        tok = torch.empty(rows, dtype=torch.int64, device=logits.device)
+        lp = torch.empty(rows, dtype=torch.float32, device=logits.device)
     _lib.check(
         _lib.lib().aios_greedy_select(logits.data_ptr(), logits.stride(0), rows, vocab,
                                       logits.element_size(), tok.data_ptr(), lp.data_ptr(),

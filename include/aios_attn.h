@@ -295,6 +295,30 @@ int aios_linear_rows_ex(const void* x, int64_t x_stride, const void* weight, int
                         void* stream);
 
 /*
+ * The per-step bookkeeping of a captured CandidateGroup decode step (the
+ * branch loop of python/aios/ime.py:1010-1054 around the model), all state
+ * in device memory so that a graph replays it:
+ *   aios_cg_step_begin: s = *step (clamped to [0, page_rows)); for every
+ *     row r: out_loc[r] = pages[s][r] and page_table[r][pos[r]] = out_loc[r]
+ *     (positions outside [0, pt_cols) are not written) -- the page the
+ *     step's K/V goes to (ime.py:1219-1251);
+ *   aios_cg_step_end: with the step's pick tok / raw: a row that is not
+ *     finished is live; a live row whose token is eos (eos >= 0) finishes
+ *     (eos_hit, finished set) and emits nothing; otherwise a live row emits:
+ *     out_ids[r][*step + 1] = tok (or -1), logp_sum += raw, counts += 1;
+ *     tokens = tok, pos += 1 for every row; fed += live rows; *step += 1.
+ * bool flags are one byte.  No reference counterpart as a single call: the
+ * reference runs these as torch ops on the host loop.
+ */
+int aios_cg_step_begin(int64_t* step, const int32_t* pages, int32_t page_rows, int32_t rows,
+                       int32_t* out_loc, int32_t* page_table, int64_t pt_stride, int32_t pt_cols,
+                       int32_t* pos, void* stream);
+int aios_cg_step_end(int64_t* step, int32_t rows, const int64_t* tok, const float* raw, int64_t eos,
+                     uint8_t* finished, uint8_t* eos_hit, int64_t* out_ids, int64_t out_stride,
+                     int32_t out_cols, float* logp_sum, int64_t* counts, int64_t* tokens,
+                     int32_t* pos, int64_t* fed, void* stream);
+
+/*
  * Greedy selection over rows of logits (elem_bytes 2: bf16, 4: fp32):
  *   token_out[r]   = first index of the maximum of logits[r, 0 .. vocab)
  *   logprob_out[r] = logits[r, token] - logsumexp(logits[r, :])  (fp32)
