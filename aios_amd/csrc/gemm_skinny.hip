@@ -177,11 +177,14 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
       }
     }
   } else {
-    for (int s0 = 0; s0 < steps; s0 += kGemmBatch) {
-      bf16x8 wa[NP][kGemmBatch];
-      bf16x8 b[kGemmBatch][MT];
+    // One row tile and one W row set: all of a 512-wide K quarter in one
+    // round trip (the down projection's K = 2048).
+    constexpr int B = (MT == 1 && NP == 1) ? 2 * kGemmBatch : kGemmBatch;
+    for (int s0 = 0; s0 < steps; s0 += B) {
+      bf16x8 wa[NP][B];
+      bf16x8 b[B][MT];
 #pragma unroll
-      for (int u = 0; u < kGemmBatch; ++u) {
+      for (int u = 0; u < B; ++u) {
         if (s0 + u < steps) {
 #pragma unroll
           for (int p = 0; p < NP; ++p)
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
         }
       }
 #pragma unroll
-      for (int u = 0; u < kGemmBatch; ++u) {
+      for (int u = 0; u < B; ++u) {
         if (s0 + u < steps) {
 #pragma unroll
           for (int p = 0; p < NP; ++p)
@@ -237,6 +240,40 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
   }
 }
 
+// Plain projections with K = 768 and up to 16 rows (the o projection and
+// LM head of hidden-768 models): one wavefront per 16 output columns over the
+// whole K, every load in one round trip, two interleaved MFMA chains, no LDS
+// reduction or barrier.
+constexpr int kColsSteps = 24;  // K = 768
+
+__global__ __launch_bounds__(64) void skinny_gemm_cols_kernel(LinearArgs a) {
+  const int lane = threadIdx.x;
+  const int l16 = lane & 15;
+  const int lg = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const bf16* wr = a.w + (n0 + l16) * a.w_stride + lg * 8;
+  const bool ok = l16 < a.M;
+  const bf16* xr = a.x + (int64_t)(ok ? l16 : 0) * a.x_stride + lg * 8;
+  bf16x8 w[kColsSteps], x[kColsSteps];
+#pragma unroll
+  for (int s = 0; s < kColsSteps; ++s) {
+    w[s] = *reinterpret_cast<const bf16x8*>(wr + s * 32);
+    x[s] = *reinterpret_cast<const bf16x8*>(xr + s * 32);
+  }
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+#pragma unroll
+  for (int s = 0; s < kColsSteps; s += 2) {
+    acc0 = mfma16x16x32(w[s], x[s], acc0);
+    acc1 = mfma16x16x32(w[s + 1], x[s + 1], acc1);
+  }
+  if (!ok) return;
+  const f32x4 o = acc0 + acc1;
+  uint2 packed;
+  packed.x = pack_bf16x2(o[0], o[1]);
+  packed.y = pack_bf16x2(o[2], o[3]);
+  *reinterpret_cast<uint2*>(a.y + (int64_t)l16 * a.y_stride + n0 + lg * 4) = packed;
+}
+
 template <int PRO, int EPI>
 hipError_t launch_pe(const LinearArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)(a.N / 16));
@@ -263,6 +300,10 @@ bool skinny_gemm_norm_supported(int64_t M, int64_t K) {
 }
 
 hipError_t skinny_gemm(const LinearArgs& a, int prologue, int epilogue, hipStream_t stream) {
+  if (prologue == kPlain && epilogue == kStore && a.M <= 16 && a.K == kColsSteps * 32) {
+    hipLaunchKernelGGL(skinny_gemm_cols_kernel, dim3((unsigned)(a.N / 16)), dim3(64), 0, stream, a);
+    return hipGetLastError();
+  }
   if (prologue == kPlain && epilogue == kStore) return launch_pe<kPlain, kStore>(a, stream);
   if (prologue == kPlain && epilogue == kSiluPair) return launch_pe<kPlain, kSiluPair>(a, stream);
   if (prologue == kAddNorm && epilogue == kStore) return launch_pe<kAddNorm, kStore>(a, stream);
