@@ -354,7 +354,7 @@ class CandidateGroupEngine:
                             seen.add(c.token_ids)
                 round_cfg = replace(config, num_candidates=attempts, sampling=sp,
                                     seed=config.seed + used * 100_003)
-                r_raw, r_alloc, r_gen, r_act, r_cancel = self._generate(
+                r_raw, r_alloc, r_gen, r_act, r_cancel = generate(
                     prefix_logits, page_table, p, round_cfg, cancellation, banned=banned)
                 unique_pages = max(unique_pages, len(prefix_pages) + sum(len(a) for a in r_alloc))
                 if r_alloc:
@@ -537,10 +537,16 @@ class CandidateGroupEngine:
             raw.append(Candidate(ids, avg, stop))
         return raw, allocated, int(sum(cnt)), active_tokens, cancelled
 
-    def _generate_graphed(self, prefix_logits, page_table, prefix_len: int, config, cancellation):
+    def _generate_graphed(self, prefix_logits, page_table, prefix_len: int, config, cancellation,
+                          banned=()):
         """The same candidate rule as :meth:`_generate`, with every decode step
         after the first replayed from a captured graph and no host
-        synchronisation until the group is done."""
+        synchronisation until the group is done.  ``banned`` (sampled rounds
+        only, at most ``_DecodeGraph.MAX_BANS``): the banned-repeat rule of
+        :meth:`_generate`, evaluated on the device each step."""
+        if banned and (config.sampling is None or len(banned) > _DecodeGraph.MAX_BANS):
+            return self._generate(prefix_logits, page_table, prefix_len, config, cancellation,
+                                  banned=banned)
         n = config.num_candidates
         t_max = config.max_new_tokens
         if cancellation.cancelled:
@@ -552,11 +558,15 @@ class CandidateGroupEngine:
         sp = config.sampling
         key = (n, t_max, plan_prefix, kv_cap, config.eos_token_id,
                None if sp is None else (sp.temperature, sp.top_k, sp.top_p),
-               config.min_new_tokens, config.blocked_ids())
+               config.min_new_tokens, config.blocked_ids(),
+               config.refill_ban_min_prefix_tokens if banned else None)
         g = self._graphs.get(key)
         if g is None:
-            g = _DecodeGraph(self, n, t_max, plan_prefix, kv_cap, config.eos_token_id, config)
+            g = _DecodeGraph(self, n, t_max, plan_prefix, kv_cap, config.eos_token_id, config,
+                             bans=bool(banned))
             self._graphs[key] = g
+        if banned:
+            g.set_bans(banned)
         allocated = []
         if t_max > 1:
             pages = self.rt.cache_manager.allocate(n * (t_max - 1))
@@ -594,8 +604,11 @@ class _DecodeGraph:
     decode metadata, runs the model, takes the argmax and advances the state.
     """
 
+    MAX_BANS = 32  # banned sequences a refill-round graph holds
+
     def __init__(self, eng: "CandidateGroupEngine", rows: int, steps: int, plan_prefix: int,
-                 kv_cap: int, eos: int | None, config: CandidateGroupConfig) -> None:
+                 kv_cap: int, eos: int | None, config: CandidateGroupConfig,
+                 bans: bool = False) -> None:
         rt = eng.rt
         dev = rt.device
         self.rt = rt
@@ -622,6 +635,15 @@ class _DecodeGraph:
         self.fed = torch.zeros(1, dtype=torch.long, device=dev)
         self.row_ids = torch.arange(rows, dtype=torch.long, device=dev)
         self.out_loc = torch.zeros(rows, dtype=torch.int32, device=dev)
+        # Banned repeats of a refill round (ime.py:977-1004): -1-padded
+        # sequences, their lengths (0: unused slot) and the minimum prefix.
+        self.bans = bans
+        if bans:
+            self.ban_ids = torch.full((self.MAX_BANS, steps), -1, dtype=torch.long, device=dev)
+            self.ban_lens = torch.zeros(self.MAX_BANS, dtype=torch.long, device=dev)
+            self.ban_cols = torch.arange(steps, dtype=torch.long, device=dev)
+            self.ban_min = torch.full((1,), config.refill_ban_min_prefix_tokens,
+                                      dtype=torch.long, device=dev)
         self.tok = torch.zeros(rows, dtype=torch.long, device=dev)
         self.raw = torch.zeros(rows, dtype=torch.float32, device=dev)
         self.md = rt.model.attn_backend.prepare_static_decode(self.row_ids, kv_cap, plan_prefix,
@@ -634,6 +656,27 @@ class _DecodeGraph:
         self.batch.positions = self.pos
         self.batch.attn_metadata = self.md
         self.graph: torch.cuda.CUDAGraph | None = None
+
+    def set_bans(self, banned) -> None:
+        ids = torch.full((self.MAX_BANS, self.steps), -1, dtype=torch.long)
+        lens = torch.zeros(self.MAX_BANS, dtype=torch.long)
+        for i, b in enumerate(banned):
+            b = b[: self.steps]
+            ids[i, : len(b)] = torch.tensor(b, dtype=torch.long)
+            lens[i] = len(b)
+        self.ban_ids.copy_(ids)
+        self.ban_lens.copy_(lens)
+
+    def _banned_next(self) -> torch.Tensor:
+        """Per-row forbidden ids of the token being sampled (index step + 1):
+        a ban's next token where the row's output so far equals the ban's
+        prefix of that length, from the minimum prefix on; -1 elsewhere."""
+        s = self.step + 1
+        eq = (self.out_ids[:, None, :] == self.ban_ids[None, :, :]) | \
+            (self.ban_cols >= s)[None, None, :]
+        match = eq.all(-1) & (self.ban_lens > s)[None, :] & (s >= self.ban_min)[None, :]
+        nxt = self.ban_ids.index_select(1, s).view(1, -1).expand(self.rows, -1)
+        return torch.where(match, nxt, torch.full_like(nxt, -1)).contiguous()
 
     def start(self, prefix_logits: torch.Tensor, prefix_len: int, seed: int) -> None:
         """Step 0: candidate i samples the prefix logits with its own uniform
@@ -680,7 +723,9 @@ class _DecodeGraph:
             logits = rt.model.forward()
         if self.sampling is not None:
             tok, raw = sample_step(logits, self.sampling, self.uni, self.step + 1, self.blocked,
-                                   self.min_new, out=(self.tok, self.raw))
+                                   self.min_new, forbidden_by_row=(self._banned_next() if self.bans
+                                                                   else None),
+                                   out=(self.tok, self.raw))
         else:
             tok, raw = greedy_select(logits, out=(self.tok, self.raw))
         _lib.check(lib.aios_cg_step_end(

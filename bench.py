@@ -194,7 +194,7 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens: int 
     ``sampling`` = (temperature, top_k, top_p) the candidates are sampled
     with stateless uniforms (the reference's candidate rule) instead of
     greedy from the top first tokens.  With ``max_candidates`` > 8, adaptive
-    refill rounds (eager steps) follow while fewer than 3 valid distinct
+    refill rounds (graph-replayed steps) follow while fewer than 3 valid distinct
     candidates exist, up to that many candidates in all.
     """
     import statistics

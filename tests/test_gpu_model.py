@@ -516,3 +516,30 @@ def test_candidate_group_adaptive_refill():
     eng._decode_step = eng.__class__._decode_step.__get__(eng)
     again = eng.complete(prefix, cfg)
     assert [x.token_ids for x in again.raw_candidates] == [x.token_ids for x in raw]
+
+
+def test_graph_replay_matches_eager_refill():
+    """Refill rounds replayed from captured graphs, with the banned-repeat
+    rule evaluated on the device, give the eager rounds' candidates."""
+    c = MINIMIND_0P1B.with_layers(4)
+    w = init_weights(c, 8, "cpu")
+    rt = CandidateGroupRuntime(c, weights_to(w, "cuda"), "cuda", num_pages=1024)
+    eager = CandidateGroupEngine(rt, use_graphs=False)
+    graphed = CandidateGroupEngine(rt, use_graphs=True)
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=8, min_new_tokens=2,
+                               sampling=SamplingParams(temperature=0.35, top_k=1, top_p=1.0),
+                               max_candidates=24)
+    for seed in (1, 2, 1):
+        prefix = _prefix(seed, 32, c.vocab_size)
+        e = eager.complete(prefix, cfg)
+        eager.reset_prefix_cache()
+        torch.cuda.synchronize()
+        g = graphed.complete(prefix, cfg)
+        graphed.reset_prefix_cache()
+        assert e.refill_rounds >= 1 and g.refill_rounds == e.refill_rounds
+        assert [x.token_ids for x in g.raw_candidates] == [x.token_ids for x in e.raw_candidates]
+        assert [x.average_logprob for x in g.raw_candidates] == \
+            [x.average_logprob for x in e.raw_candidates]
+        greedy = g.raw_candidates[0].token_ids
+        assert all(x.token_ids != greedy for x in g.raw_candidates[8:])
+    assert rt.cache_manager.available_size == rt.num_pages
