@@ -543,3 +543,26 @@ def test_graph_replay_matches_eager_refill():
         greedy = g.raw_candidates[0].token_ids
         assert all(x.token_ids != greedy for x in g.raw_candidates[8:])
     assert rt.cache_manager.available_size == rt.num_pages
+
+
+def test_refill_budget_and_deadline():
+    """The attempt budget caps a refill round (8 + 2 of max 10), and a
+    deadline already passed when the first round ends stops refill
+    (ime.py:511-517)."""
+    c = MINIMIND_0P1B.with_layers(2)
+    w = init_weights(c, 5, "cpu")
+    rt = CandidateGroupRuntime(c, weights_to(w, "cuda"), "cuda", num_pages=512)
+    eng = CandidateGroupEngine(rt, use_graphs=True)
+    base = dict(num_candidates=8, max_new_tokens=6, min_new_tokens=2,
+                sampling=SamplingParams(temperature=0.35, top_k=1, top_p=1.0))
+    prefix = _prefix(3, 16, c.vocab_size)
+    r = eng.complete(prefix, CandidateGroupConfig(max_candidates=10, **base))
+    eng.reset_prefix_cache()
+    assert r.refill_rounds == 1 and len(r.raw_candidates) == 10
+    r = eng.complete(prefix, CandidateGroupConfig(max_candidates=24, refill_deadline_ms=1e-6,
+                                                  **base))
+    eng.reset_prefix_cache()
+    assert r.refill_rounds == 0 and len(r.raw_candidates) == 8
+    # one distinct valid candidate: the display set holds it once
+    assert [x.token_ids for x in r.candidates] == [r.raw_candidates[0].token_ids]
+    assert rt.cache_manager.available_size == rt.num_pages
