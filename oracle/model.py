@@ -21,6 +21,11 @@ for a token sequence:
 Everything is float32 (weights are the same bf16 values, widened), attention
 is dense over the whole sequence, so the paged/cascade decomposition of the
 product path does not appear here at all.
+
+Pinning: the standard trunk equals transformers' Qwen3ForCausalLM on the same
+weights (tests/test_oracle_hf.py).  The Block-AttnRes trunk composition is
+parity unpinned: no independent implementation or reference fixture of it
+exists offline.
 """
 from __future__ import annotations
 
