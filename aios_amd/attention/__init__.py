@@ -4,6 +4,7 @@ from .backend import (
     Mi355xAttentionBackend,
     Mi355xAttentionMetadata,
     Mi355xStaticDecodeMetadata,
+    check_decode_preconditions,
 )
 
 __all__ = [
@@ -14,4 +15,5 @@ __all__ = [
     "Mi355xAttentionMetadata",
     "Mi355xStaticDecodeMetadata",
     "SUPPORTED_HEAD_DIMS",
+    "check_decode_preconditions",
 ]

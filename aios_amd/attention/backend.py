@@ -11,15 +11,25 @@ Public surface follows python/aios/attention/flashinfer.py:94-394:
 * ``forward(q, k, v, kv_cache, layer_id, batch)`` appends the new K/V rows
   (kernel (a)) and then runs prefill (kernel (b)) or decode (kernels (c),
   (d) and the combine) through the C ABI, returning ``[tokens, Hq*D]``; a
-  decode step appends inside the decode launch (aios_attn_append_decode).
+  decode batch marked ``fused_append`` appends inside the decode launch
+  (aios_attn_append_decode).
 * ``metadata.get_last_indices(bs)`` = ``cu_seqlens_q[1:bs+1] - 1``.
 
 There is one code path for every supported head dim (64, 96, 128), so the
 reference's torch-SDPA fallback for head_dim 96 (flashinfer.py:19-24,
 328-372) has no counterpart here.
+
+Two caller guarantees change what a decode does, and both are opt-in on the
+batch: ``Batch.shared_prefix_len`` lets the prefix pages be read once per
+kv-head (the cascade), and ``Batch.fused_append`` lets the K/V append run
+inside the decode launch.  ``validate=True`` (or ``AIOS_VALIDATE=1``) checks
+both on the first layer of every eagerly run decode batch
+(:func:`check_decode_preconditions`, one host synchronisation) and raises
+``ValueError`` when the batch breaks them; captured graphs skip the check.
 """
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 from typing import TYPE_CHECKING
 
@@ -91,6 +101,35 @@ class Mi355xStaticDecodeMetadata(Mi355xAttentionMetadata):
         )
 
 
+def check_decode_preconditions(indices: torch.Tensor, cu_seqlens_k: torch.Tensor,
+                               out_loc: torch.Tensor | None, shared_prefix_len: int) -> None:
+    """Raise ``ValueError`` unless the decode batch keeps the caller
+    guarantees the backend relies on: every row's first
+    ``shared_prefix_len`` page ids equal row 0's, and (``out_loc`` given, the
+    fused append) ``out_loc[b]`` is row b's last page id,
+    ``indices[cu_seqlens_k[b + 1] - 1]``.  Works on CPU or device tensors;
+    one host synchronisation for device tensors."""
+    cu = cu_seqlens_k.to(torch.long)
+    bs = cu.numel() - 1
+    if bs <= 0:
+        return
+    lens = cu[1:] - cu[:-1]
+    if shared_prefix_len > 0:
+        if bool((lens < shared_prefix_len).any()):
+            raise ValueError(f"shared_prefix_len {shared_prefix_len} exceeds a row's KV length")
+        ar = torch.arange(shared_prefix_len, device=indices.device)
+        rows = indices[cu[:-1, None] + ar[None, :]]
+        if not bool((rows == rows[:1]).all()):
+            raise ValueError(f"rows do not share their first {shared_prefix_len} pages "
+                             "(Batch.shared_prefix_len)")
+    if out_loc is not None:
+        if bool((lens < 1).any()):
+            raise ValueError("a decode row has no KV position for its new token")
+        last = indices[cu[1:] - 1]
+        if not bool((out_loc.to(last.dtype) == last).all()):
+            raise ValueError("out_loc[b] must be row b's last page id (Batch.fused_append)")
+
+
 class Mi355xAttentionBackend(BaseAttentionBackend):
     """Paged prefill/decode on hand-written gfx950 HIP kernels."""
 
@@ -100,6 +139,7 @@ class Mi355xAttentionBackend(BaseAttentionBackend):
         workspace_size: int = 128 * 1024 * 1024,
         prefix_chunk_len: int = 0,
         suffix_split_len: int = 0,
+        validate: bool | None = None,
     ) -> None:
         self.num_heads = config.num_qo_heads
         self.num_kv_heads = config.num_kv_heads
@@ -119,6 +159,8 @@ class Mi355xAttentionBackend(BaseAttentionBackend):
         self.workspace_size = workspace_size
         self.prefix_chunk_len = prefix_chunk_len
         self.suffix_split_len = suffix_split_len
+        self.validate = (os.environ.get("AIOS_VALIDATE", "0") not in ("", "0")
+                         if validate is None else bool(validate))
         self._workspace: torch.Tensor | None = None
         self._cached_ones_cpu: torch.Tensor = torch.tensor([], dtype=torch.int32)
 
@@ -331,9 +373,15 @@ class Mi355xAttentionBackend(BaseAttentionBackend):
         plan = metadata.plan
         out_loc = batch.out_loc.view(-1)
         ws = self._get_workspace(q.device) if plan.ws_bytes else None
-        if plan.prefix_len < plan.min_kv_len and out_loc.dtype == torch.int32:
+        fused = (batch.fused_append and plan.prefix_len < plan.min_kv_len
+                 and out_loc.dtype == torch.int32)
+        if self.validate and layer_id == 0 and not torch.cuda.is_current_stream_capturing():
+            check_decode_preconditions(metadata.indices, metadata.cu_seqlens_k_gpu,
+                                       out_loc if fused else None, metadata.shared_prefix_len)
+        if fused:
             # The store_kv of flashinfer.py:389 runs inside the decode launch:
-            # each row's new token is its last KV position.
+            # the caller guarantees (Batch.fused_append) that each row's new
+            # token goes to its last KV position's page.
             if k.shape != v.shape or k.shape[1:] != (self.num_kv_heads, self.head_dim):
                 raise ValueError("K/V input shape does not match the cache layout")
             if out_loc.numel() != k.shape[0]:

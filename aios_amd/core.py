@@ -2,10 +2,16 @@
 
 Mirrors python/aios/core.py:14-124 (SamplingParams, Req, Batch, Context and
 the process-global context) so that callers written against the reference
-drive this backend unchanged.  One field is added: ``Batch.shared_prefix_len``
-(default 0), the number of leading KV positions whose pages every row of a
-decode batch shares; the CandidateGroup engine sets it (the reference creates
-that sharing at python/aios/ime.py:1155 but never tells the backend).
+drive this backend unchanged.  Two fields are added, both set only by callers
+that guarantee what they state (the CandidateGroup engine here):
+
+* ``Batch.shared_prefix_len`` (default 0): the number of leading KV positions
+  whose pages every row of a decode batch shares (the reference creates that
+  sharing at python/aios/ime.py:1155 but never tells the backend);
+* ``Batch.fused_append`` (default False): every decode row's ``out_loc`` entry
+  is that row's last page, ``page_table[row, device_len - 1]`` (as in
+  ime.py:1228-1229), so the backend may append the new K/V inside the decode
+  launch instead of running ``store_kv`` first (flashinfer.py:389).
 """
 from __future__ import annotations
 
@@ -81,6 +87,7 @@ class Batch:
     attn_metadata: "BaseAttentionMetadata" = field(init=False)
     return_all_logits: bool = False
     shared_prefix_len: int = 0
+    fused_append: bool = False
 
     @property
     def is_prefill(self) -> bool:

@@ -33,6 +33,7 @@ from __future__ import annotations
 import math
 import threading
 import time
+from collections import OrderedDict
 from dataclasses import dataclass, field, replace
 
 import torch
@@ -102,6 +103,10 @@ class CandidateGroupConfig:
     refill_avoid_exact_repeats: bool = True
     refill_ban_min_prefix_tokens: int = 2
     refill_deadline_ms: float = 0.0  # no new round after this wall time (0: none)
+    # Fill of the per-row banned-id table where no banned sequence matches
+    # (ime.py:990-996 fills with the tokenizer's pad id, so during the ban
+    # window every row is also forbidden the pad id); None: no fill id.
+    pad_token_id: int | None = None
 
     def validate(self) -> None:
         if self.num_candidates < self.display_candidates or self.display_candidates < 1:
@@ -167,6 +172,19 @@ def adaptive_refill_attempts(candidates, config: CandidateGroupConfig, attempts_
     predicted = math.ceil(deficit / max(floor, observed))
     planned = max(config.min_refill_batch_size, deficit * 2, predicted)
     return min(planned, config.refill_batch_size, remaining)
+
+
+def banned_next_ids(out_ids: torch.Tensor, step: int, ban_ids: torch.Tensor,
+                    ban_lens: torch.Tensor, fill: int) -> torch.Tensor:
+    """Per-row forbidden ids at token index ``step`` (ime.py:977-996): for
+    every banned sequence j, its token ``step`` where the row's first
+    ``step`` outputs equal the sequence's and the sequence is longer than
+    ``step``; ``fill`` elsewhere.  out_ids [rows, >= step], ban_ids
+    [bans, >= step + 1] -> [rows, bans]."""
+    match = (out_ids[:, None, :step] == ban_ids[None, :, :step]).all(-1)
+    match &= ban_lens[None, :] > step
+    nxt = ban_ids[None, :, step].expand(out_ids.shape[0], -1)
+    return torch.where(match, nxt, torch.full_like(nxt, fill)).contiguous()
 
 
 @dataclass(frozen=True)
@@ -251,10 +269,19 @@ class CandidateGroupEngine:
     hit EOS are then masked instead of compacted.  ``use_graphs=False`` runs
     the eager loop with the reference's row compaction."""
 
+    # Captured decode graphs kept at once (least recently used dropped first:
+    # each holds its own memory pool, and keys grow with prefix length,
+    # round size and refill sampling parameters).
+    MAX_GRAPHS = 12
+    # Graph-replayed steps the host queues ahead of the GPU: cancellation is
+    # observed before each step is queued, so a superseded keystroke stops
+    # within this many steps.
+    RUN_AHEAD = 3
+
     def __init__(self, rt: CandidateGroupRuntime, use_graphs: bool = True) -> None:
         self.rt = rt
         self.use_graphs = use_graphs
-        self._graphs: dict[tuple, _DecodeGraph] = {}
+        self._graphs: OrderedDict[tuple, _DecodeGraph] = OrderedDict()
         self._generation_id = 0
         self._active: CancellationToken | None = None
         self._gen_lock = threading.Lock()
@@ -442,6 +469,7 @@ class CandidateGroupEngine:
         batch.positions = torch.full((len(rows),), cached_len, dtype=torch.int32, device=dev)
         batch.out_loc = pages
         batch.shared_prefix_len = prefix_len
+        batch.fused_append = True  # pages[i] is row i's last page (set above)
         self.rt.model.attn_backend.prepare_metadata(batch)
         with self.rt.ctx.forward_batch(batch):
             logits = self.rt.model.forward()
@@ -476,14 +504,13 @@ class CandidateGroupEngine:
                     ban_ids[i, : len(b)] = torch.tensor(b, dtype=torch.long, device=dev)
                 ban_lens = torch.tensor([len(b) for b in banned], dtype=torch.long, device=dev)
 
+            fill = -1 if config.pad_token_id is None else int(config.pad_token_id)
+
             def pick(logits, rows, step):
                 col = torch.full((1,), step, dtype=torch.int64, device=dev)
                 by_row = None
                 if banned and config.refill_ban_min_prefix_tokens <= step < ban_len:
-                    match = (out_ids[rows, :step][:, None, :] == ban_ids[None, :, :step]).all(-1)
-                    match &= ban_lens[None, :] > step
-                    nxt = ban_ids[None, :, step].expand(len(rows), -1)
-                    by_row = torch.where(match, nxt, torch.full_like(nxt, -1)).contiguous()
+                    by_row = banned_next_ids(out_ids[rows], step, ban_ids, ban_lens, fill)
                 return sample_step(logits, config.sampling, uni[rows], col, blocked_t,
                                    config.min_new_tokens, forbidden_by_row=by_row)
 
@@ -559,12 +586,15 @@ class CandidateGroupEngine:
         key = (n, t_max, plan_prefix, kv_cap, config.eos_token_id,
                None if sp is None else (sp.temperature, sp.top_k, sp.top_p),
                config.min_new_tokens, config.blocked_ids(),
-               config.refill_ban_min_prefix_tokens if banned else None)
+               (config.refill_ban_min_prefix_tokens, config.pad_token_id) if banned else None)
         g = self._graphs.get(key)
         if g is None:
+            while len(self._graphs) >= self.MAX_GRAPHS:
+                self._graphs.popitem(last=False)  # drops the graph and its pool
             g = _DecodeGraph(self, n, t_max, plan_prefix, kv_cap, config.eos_token_id, config,
                              bans=bool(banned))
             self._graphs[key] = g
+        self._graphs.move_to_end(key)
         if banned:
             g.set_bans(banned)
         allocated = []
@@ -574,11 +604,20 @@ class CandidateGroupEngine:
             g.pages[: t_max - 1].copy_(pages.view(t_max - 1, n))
         g.start(prefix_logits, prefix_len, config.seed)
         cancelled = False
-        for _ in range(t_max - 1):
-            if cancellation.cancelled:  # observed between steps (ime.py:971-973)
+        queued: list[torch.cuda.Event] = []
+        for i in range(t_max - 1):
+            # Observed between steps (ime.py:971-973): the host waits until at
+            # most RUN_AHEAD steps are queued, so a cancel stops the group
+            # within that many steps instead of after every step was queued.
+            if i >= self.RUN_AHEAD:
+                queued[i - self.RUN_AHEAD].synchronize()
+            if cancellation.cancelled:
                 cancelled = True
                 break
             g.run_step()
+            ev = torch.cuda.Event()
+            ev.record()
+            queued.append(ev)
         ids = g.out_ids.cpu()
         cnt = g.counts.cpu().tolist()
         sums = g.logp_sum.cpu().tolist()
@@ -644,6 +683,8 @@ class _DecodeGraph:
             self.ban_cols = torch.arange(steps, dtype=torch.long, device=dev)
             self.ban_min = torch.full((1,), config.refill_ban_min_prefix_tokens,
                                       dtype=torch.long, device=dev)
+            self.ban_fill = -1 if config.pad_token_id is None else int(config.pad_token_id)
+            self.ban_max = torch.zeros(1, dtype=torch.long, device=dev)  # longest ban
         self.tok = torch.zeros(rows, dtype=torch.long, device=dev)
         self.raw = torch.zeros(rows, dtype=torch.float32, device=dev)
         self.md = rt.model.attn_backend.prepare_static_decode(self.row_ids, kv_cap, plan_prefix,
@@ -652,6 +693,9 @@ class _DecodeGraph:
                     sampling_params=SamplingParams(max_tokens=1), table_idx=r)
                 for r in range(rows)]
         self.batch = Batch(reqs=reqs, phase="decode")
+        # aios_cg_step_begin writes each row's page into both out_loc and the
+        # page-table column the step attends to last
+        self.batch.fused_append = True
         self.batch.input_ids = self.tokens
         self.batch.positions = self.pos
         self.batch.attn_metadata = self.md
@@ -666,17 +710,22 @@ class _DecodeGraph:
             lens[i] = len(b)
         self.ban_ids.copy_(ids)
         self.ban_lens.copy_(lens)
+        self.ban_max.fill_(int(lens.max()))
 
     def _banned_next(self) -> torch.Tensor:
         """Per-row forbidden ids of the token being sampled (index step + 1):
         a ban's next token where the row's output so far equals the ban's
-        prefix of that length, from the minimum prefix on; -1 elsewhere."""
+        prefix of that length, from the minimum prefix on; the pad id (or
+        -1, none) elsewhere while a ban is that long (ime.py:977-996), -1
+        outside that window."""
         s = self.step + 1
         eq = (self.out_ids[:, None, :] == self.ban_ids[None, :, :]) | \
             (self.ban_cols >= s)[None, None, :]
-        match = eq.all(-1) & (self.ban_lens > s)[None, :] & (s >= self.ban_min)[None, :]
+        window = (s >= self.ban_min) & (s < self.ban_max)
+        match = eq.all(-1) & (self.ban_lens > s)[None, :] & window[None, :]
         nxt = self.ban_ids.index_select(1, s).view(1, -1).expand(self.rows, -1)
-        return torch.where(match, nxt, torch.full_like(nxt, -1)).contiguous()
+        fill = torch.where(window, self.ban_fill, -1).view(1, 1)
+        return torch.where(match, nxt, fill.expand_as(nxt)).contiguous()
 
     def start(self, prefix_logits: torch.Tensor, prefix_len: int, seed: int) -> None:
         """Step 0: candidate i samples the prefix logits with its own uniform

@@ -299,10 +299,10 @@ def test_layer_cache_above_4gib_is_rejected():
     kc = wl.k_cache[0].to(DEV)
     ws = torch.empty(max(p.ws_bytes, 1), dtype=torch.uint8, device=DEV)
     pages = (1 << 32) // (p.num_kv_heads * p.head_dim * 2)
+    idx, cu_k = wl.indices.to(DEV), wl.cu_k.to(DEV)
     status = _lib.lib().aios_attn_decode(
-        p, q.data_ptr(), q.stride(0), kc.data_ptr(), kc.data_ptr(), pages,
-        wl.indices.to(DEV).data_ptr(), wl.cu_k.to(DEV).data_ptr(), out.data_ptr(),
-        ws.data_ptr(), ws.numel(), p.head_dim ** -0.5, None)
+        p, q.data_ptr(), q.stride(0), kc.data_ptr(), kc.data_ptr(), pages, idx.data_ptr(),
+        cu_k.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), p.head_dim ** -0.5, None)
     assert status == _lib.AIOS_ERR_UNSUPPORTED
     assert "4 GiB" in _lib.lib().aios_last_error().decode()
 

@@ -566,3 +566,103 @@ def test_refill_budget_and_deadline():
     # one distinct valid candidate: the display set holds it once
     assert [x.token_ids for x in r.candidates] == [r.raw_candidates[0].token_ids]
     assert rt.cache_manager.available_size == rt.num_pages
+
+
+def test_graph_refill_pad_fill_matches_eager():
+    """With the tokenizer's pad id as the ban-table fill (ime.py:990-996),
+    graph-replayed refill rounds equal the eager ones, and inside the ban
+    window no refill row takes the pad id."""
+    c = MINIMIND_0P1B.with_layers(3)
+    w = init_weights(c, 8, "cpu")
+    rt = CandidateGroupRuntime(c, weights_to(w, "cuda"), "cuda", num_pages=1024)
+    eager = CandidateGroupEngine(rt, use_graphs=False)
+    graphed = CandidateGroupEngine(rt, use_graphs=True)
+    prefix = _prefix(2, 32, c.vocab_size)
+    base = CandidateGroupConfig(num_candidates=8, max_new_tokens=8, min_new_tokens=2,
+                                sampling=SamplingParams(temperature=0.35, top_k=1, top_p=1.0),
+                                max_candidates=16)
+    probe = graphed.complete(prefix, base)
+    graphed.reset_prefix_cache()
+    # the pad id: a token the unpadded refill round takes inside the window
+    window = [t for x in probe.raw_candidates[8:] for t in x.token_ids[2:]]
+    assert window
+    pad = max(set(window), key=window.count)
+    cfg = replace(base, pad_token_id=pad)
+    e = eager.complete(prefix, cfg)
+    eager.reset_prefix_cache()
+    g = graphed.complete(prefix, cfg)
+    graphed.reset_prefix_cache()
+    assert g.refill_rounds == e.refill_rounds >= 1
+    assert [x.token_ids for x in g.raw_candidates] == [x.token_ids for x in e.raw_candidates]
+    greedy_len = len(g.raw_candidates[0].token_ids)
+    for x in g.raw_candidates[8:]:
+        assert pad not in x.token_ids[2:greedy_len]
+    assert rt.cache_manager.available_size == rt.num_pages
+
+
+def test_graph_cache_is_bounded():
+    """Captured decode graphs are kept in a least-recently-used cache of
+    MAX_GRAPHS entries: many group shapes do not grow device memory without
+    bound, and a re-used shape keeps its graph."""
+    c = MINIMIND_0P1B.with_layers(2)
+    eng, _ = _engine(c, 4, num_pages=2048, use_graphs=True)
+    prefix = _prefix(4, 24, c.vocab_size)
+    cap = eng.MAX_GRAPHS
+    mem = []
+    for t in range(2, cap + 8):
+        eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=t))
+        assert len(eng._graphs) <= cap
+        torch.cuda.synchronize()
+        mem.append(torch.cuda.memory_allocated())
+    assert len(eng._graphs) == cap
+    # after the cache is full, further shapes evict: memory stays at the
+    # level of a full cache (plus one larger graph at most)
+    per_graph = (mem[cap - 1] - mem[0]) / (cap - 1)
+    assert mem[-1] <= mem[cap - 1] + 2 * max(per_graph, 1 << 20)
+    # an older shape still in the cache is reused (and becomes the newest)
+    key = next(k for k in eng._graphs if k[1] == cap + 3)
+    g = eng._graphs[key]
+    eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=cap + 3))
+    assert next(reversed(eng._graphs)) == key and eng._graphs[key] is g
+    assert len(eng._graphs) == cap
+    eng.reset_prefix_cache()
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages
+
+
+class _CancelAfter(CancellationToken):
+    """Reads as cancelled from the n-th look on (a cancel that arrives while
+    the group runs, without timing)."""
+
+    def __init__(self, n):
+        super().__init__(0)
+        self.n = n
+        self.looks = 0
+
+    @property
+    def cancelled(self):
+        self.looks += 1
+        return self.looks >= self.n
+
+
+@pytest.mark.parametrize("use_graphs", [False, True])
+def test_cancel_mid_group_stops_decoding(use_graphs):
+    """Latest-wins cancellation is observed between decode steps
+    (ime.py:971-973) in eager and graph-replayed groups: the result is
+    marked cancelled, the candidates stop early, pages are all returned."""
+    c = MINIMIND_0P1B.with_layers(2)
+    eng, _ = _engine(c, 6, use_graphs=use_graphs)
+    prefix = _prefix(6, 20, c.vocab_size)
+    t = 16
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=t)
+    full = eng.complete(prefix, cfg)
+    assert not full.cancelled
+    assert all(len(x.token_ids) == t for x in full.raw_candidates)
+    res = eng.complete(prefix, cfg, cancellation=_CancelAfter(6))
+    assert res.cancelled
+    assert all(x.stop_reason == "cancelled" for x in res.raw_candidates)
+    assert all(1 <= len(x.token_ids) < t // 2 for x in res.raw_candidates)
+    # what was produced before the cancel is the uncancelled group's start
+    for a, b in zip(res.raw_candidates, full.raw_candidates):
+        assert a.token_ids == b.token_ids[: len(a.token_ids)]
+    eng.reset_prefix_cache()
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages

@@ -120,3 +120,44 @@ def test_candidate_validity():
 def test_refill_config_validation(kw, msg):
     with pytest.raises(ValueError, match=msg):
         CandidateGroupConfig(num_candidates=8, **kw).validate()
+
+
+def test_decode_preconditions_checker():
+    """check_decode_preconditions accepts a CandidateGroup-shaped batch and
+    rejects a wrong out_loc or rows that do not share the claimed prefix."""
+    from aios_amd.attention import check_decode_preconditions
+
+    prefix = [9, 4, 7]
+    rows = [prefix + [20, 21], prefix + [30], prefix + [40, 41, 42]]
+    indices = torch.tensor(sum(rows, []), dtype=torch.int32)
+    cu_k = torch.tensor([0, 5, 9, 15], dtype=torch.int32)
+    out_loc = torch.tensor([21, 30, 42], dtype=torch.int32)
+    check_decode_preconditions(indices, cu_k, out_loc, 3)
+    check_decode_preconditions(indices, cu_k, None, 3)
+    check_decode_preconditions(indices, cu_k, out_loc, 0)
+    with pytest.raises(ValueError, match="last page"):
+        check_decode_preconditions(indices, cu_k, torch.tensor([21, 31, 42], dtype=torch.int32), 3)
+    with pytest.raises(ValueError, match="share"):
+        check_decode_preconditions(indices, cu_k, out_loc, 4)  # row 0 has 20, row 1 has 30
+    bad = indices.clone()
+    bad[6] = 5  # row 1's second prefix page
+    with pytest.raises(ValueError, match="share"):
+        check_decode_preconditions(bad, cu_k, None, 3)
+    with pytest.raises(ValueError, match="exceeds"):
+        check_decode_preconditions(indices, cu_k, None, 5)
+
+
+def test_banned_next_ids_hand_case():
+    """ime.py:977-996 worked by hand: at step 2, row 0 has produced [5, 6]
+    (ban 0 = [5, 6, 7] matches -> 7), row 1 [5, 9] (no ban matches); ban 1 =
+    [5, 6] is not longer than the step, so it never applies; the other
+    slots hold the fill (the pad id, or -1 for none)."""
+    from aios_amd.ime import banned_next_ids
+
+    out = torch.tensor([[5, 6, -1], [5, 9, -1]])
+    bans = torch.tensor([[5, 6, 7], [5, 6, -1]])
+    lens = torch.tensor([3, 2])
+    assert banned_next_ids(out, 2, bans, lens, 0).tolist() == [[7, 0], [0, 0]]
+    assert banned_next_ids(out, 2, bans, lens, -1).tolist() == [[7, -1], [-1, -1]]
+    # step 1: both rows match ban 0's first token and ban 1's
+    assert banned_next_ids(out, 1, bans, lens, 3).tolist() == [[6, 6], [6, 6]]
