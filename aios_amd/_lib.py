@@ -25,6 +25,10 @@ EPILOGUE_NONE = 0
 EPILOGUE_SILU_MUL = 1
 
 # Every symbol include/aios_attn.h declares.
+# Size of the built-in partial-state array of aios_attn_decode_noalloc
+# (AIOS_DECODE_NOALLOC_MAX_BYTES in include/aios_attn.h).
+DECODE_NOALLOC_MAX_BYTES = 8 << 20
+
 EXPORTED_SYMBOLS = (
     "aios_last_error",
     "aios_version",
@@ -33,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "aios_attn_prefill",
     "aios_attn_decode",
     "aios_attn_append_decode",
+    "aios_attn_decode_noalloc",
     "aios_build_indices",
     "aios_rmsnorm",
     "aios_qk_norm_rope",
@@ -116,6 +121,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.aios_attn_decode.restype = ctypes.c_int
     lib.aios_attn_decode.argtypes = [
         ctypes.POINTER(AttnPlan), _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _f32, _vp,
+    ]
+    lib.aios_attn_decode_noalloc.restype = ctypes.c_int
+    lib.aios_attn_decode_noalloc.argtypes = [
+        ctypes.POINTER(AttnPlan), _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _f32, _vp,
     ]
     lib.aios_attn_append_decode.restype = ctypes.c_int
     lib.aios_attn_append_decode.argtypes = [

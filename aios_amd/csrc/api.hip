@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/aios_attn.h"
 #include "kernels.hpp"
 
@@ -383,6 +385,75 @@ int aios_attn_append_decode(const aios_attn_plan_t* p, const void* q, int64_t q_
   const NewKV nk = {k_new, k_tok_stride, v_new, v_tok_stride, out_loc};
   return decode_impl(p, q, q_tok_stride, k_cache, v_cache, kv_num_pages, indices, cu_k, out,
                      workspace, workspace_bytes, sm_scale, stream, &nk);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode.  The partial softmax states live in this file-scope
+// device array instead of a caller workspace: every GPU the library runs on
+// holds its own copy until the process ends.  Host code never uses the
+// array's name as an address (on the host it is only a stand-in); the
+// device address of the current GPU's copy is looked up once per device with
+// hipGetSymbolAddress and passed to the kernels like a workspace.
+constexpr int64_t kNoAllocScratchBytes = AIOS_DECODE_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address (looked up on its first use there).
+// The stream must belong to the current device.
+int scratch_for(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return check_hip(e, "decode_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(AIOS_ERR_UNSUPPORTED, "decode_noalloc: device %d beyond the %d supported", dev,
+                kMaxDevices);
+  if (stream) {
+    int sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) return check_hip(e, "decode_noalloc: hipStreamGetDevice");
+    if (sdev != dev)
+      return fail(AIOS_ERR_INVALID, "decode_noalloc: stream of device %d, current device %d",
+                  sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return check_hip(e, "decode_noalloc: hipGetSymbolAddress(scratch)");
+    if (!p || ((uintptr_t)p & 255) != 0)
+      return fail(AIOS_ERR_LAUNCH, "decode_noalloc: scratch address %p not 256-byte aligned", p);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return AIOS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aios_attn_decode_noalloc(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
+                             const void* k_cache, const void* v_cache, int64_t kv_num_pages,
+                             const int32_t* indices, const int32_t* cu_k, void* out,
+                             float sm_scale, void* stream) {
+  int rc = check_plan(p, AIOS_PHASE_DECODE);
+  if (rc) return rc;
+  if (p->ws_bytes > kNoAllocScratchBytes)
+    return fail(AIOS_ERR_WORKSPACE,
+                "decode_noalloc: the batch needs %lld bytes of partial states, above the %lld "
+                "of the built-in scratch (use aios_attn_decode with a workspace)",
+                (long long)p->ws_bytes, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if ((rc = scratch_for(stream, &ws))) return rc;
+  return decode_impl(p, q, q_tok_stride, k_cache, v_cache, kv_num_pages, indices, cu_k, out, ws,
+                     kNoAllocScratchBytes, sm_scale, stream, nullptr);
 }
 
 int aios_build_indices(const int32_t* page_table, int64_t page_table_stride,

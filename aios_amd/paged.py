@@ -95,6 +95,34 @@ def decode(p: _lib.AttnPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
     return out
 
 
+def decode_noalloc(p: _lib.AttnPlan, q: torch.Tensor, k_cache: torch.Tensor,
+                   v_cache: torch.Tensor, indices: torch.Tensor, cu_k: torch.Tensor, *,
+                   out: torch.Tensor, sm_scale: float | None = None) -> torch.Tensor:
+    """``decode`` with the partial states in the library's built-in device
+    array (aios_attn_decode_noalloc): no workspace and no allocation, so the
+    caller passes ``out``.  Calls overlapping on one GPU race."""
+    if p.phase != _lib.PHASE_DECODE:
+        raise ValueError("plan was not built for decode")
+    _check_q(q, p)
+    if q.shape[0] != p.batch_size:
+        raise ValueError("decode batch must contain one flat token per request")
+    _check_cache(k_cache, p)
+    _check_cache(v_cache, p)
+    _check_i32(indices, "indices", p.total_kv)
+    _check_i32(cu_k, "cu_k", p.batch_size + 1)
+    if out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bfloat16 tensor shaped like q")
+    scale = p.head_dim ** -0.5 if sm_scale is None else sm_scale
+    _lib.check(
+        _lib.lib().aios_attn_decode_noalloc(
+            p, q.data_ptr(), q.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+            k_cache.shape[0], indices.data_ptr(), cu_k.data_ptr(), out.data_ptr(), scale,
+            _stream(q.device)),
+        "aios_attn_decode_noalloc",
+    )
+    return out
+
+
 def _check_new_kv(k: torch.Tensor, v: torch.Tensor, out_loc: torch.Tensor, p: _lib.AttnPlan) -> None:
     if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16 or not k.is_cuda or not v.is_cuda:
         raise ValueError("new K/V rows must be bfloat16 GPU tensors")

@@ -208,6 +208,27 @@ int aios_attn_append_decode(const aios_attn_plan_t* plan, const void* q,
                             float sm_scale, void* stream);
 
 /*
+ * aios_attn_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The partial softmax states live in a device array built into the library
+ * (AIOS_DECODE_NOALLOC_MAX_BYTES per GPU, held until the process ends); a
+ * plan whose ws_bytes exceeds it returns AIOS_ERR_WORKSPACE.  The call
+ * allocates nothing (no hipMalloc / hipFree); its first call on a device
+ * looks up that device's array once.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (concurrent streams or
+ * threads) race.  Nothing in the array needs to start at zero: every
+ * partial the combine reads is written by the same call.  The stream must
+ * belong to the current device.  Same results as aios_attn_decode.
+ */
+#define AIOS_DECODE_NOALLOC_MAX_BYTES (8ll << 20)
+int aios_attn_decode_noalloc(const aios_attn_plan_t* plan, const void* q,
+                             int64_t q_tok_stride, const void* k_cache,
+                             const void* v_cache, int64_t kv_num_pages,
+                             const int32_t* indices, const int32_t* cu_k,
+                             void* out, float sm_scale, void* stream);
+
+/*
  * Gather the flat page-index list of a batch on the device:
  *   indices_out[cu_k[b] + j] = page_table[row_ids[b] * page_table_stride + j]
  * for j in [0, cu_k[b+1] - cu_k[b]).  row_ids and cu_k are device int32.

@@ -124,3 +124,9 @@ def test_check_maps_status_to_exceptions():
     rc, _ = _plan(_lib.PHASE_DECODE, [0, 2], [0, 5])
     with pytest.raises(ValueError, match="one flat token"):
         _lib.check(rc, "plan")
+
+
+def test_noalloc_limit_matches_header():
+    text = HEADER.read_text()
+    m = re.search(r"#define AIOS_DECODE_NOALLOC_MAX_BYTES \((\d+)ll << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.DECODE_NOALLOC_MAX_BYTES
