@@ -208,6 +208,12 @@ class CompletionResult:
     cancelled: bool
     prefix_logits: torch.Tensor | None = field(default=None, repr=False)
     refill_rounds: int = 0
+    # GPU-event time of the prefix prefill or LCP extension (0 when the
+    # cached prefix logits were reused), and of the graph-replayed decode
+    # steps of every round with their count (graph mode only).
+    prefill_gpu_ms: float = 0.0
+    replay_gpu_ms: float = 0.0
+    replayed_steps: int = 0
 
 
 def select_top(candidates, k: int) -> tuple[Candidate, ...]:
@@ -289,6 +295,7 @@ class CandidateGroupEngine:
         self._prefix_ids: list[int] = []
         self._prefix_pages: torch.Tensor | None = None
         self._prefix_logits: torch.Tensor | None = None
+        self._replay = [0.0, 0]  # this call's replayed-step GPU ms and count
 
     # -- lifecycle -------------------------------------------------------------
     def new_generation(self) -> CancellationToken:
@@ -343,9 +350,12 @@ class CandidateGroupEngine:
         started = torch.cuda.Event(enable_timing=True)
         ended = torch.cuda.Event(enable_timing=True)
         started.record()
+        prefilled = torch.cuda.Event(enable_timing=True)
+        self._replay = [0.0, 0]
         allocated: list[torch.Tensor] = []
         try:
             prefix_logits, prefix_pages, reused = self._prepare_prefix(token_ids, page_table)
+            prefilled.record()
             generate = self._generate_graphed if self.use_graphs else self._generate
             raw, allocated, generated, active_tokens, cancelled = generate(
                 prefix_logits, page_table, p, config, cancellation)
@@ -408,6 +418,9 @@ class CandidateGroupEngine:
                 cancelled=cancelled,
                 prefix_logits=prefix_logits,
                 refill_rounds=rounds,
+                prefill_gpu_ms=started.elapsed_time(prefilled) if reused < p else 0.0,
+                replay_gpu_ms=self._replay[0],
+                replayed_steps=self._replay[1],
             )
         finally:
             if allocated:
@@ -605,6 +618,8 @@ class CandidateGroupEngine:
         g.start(prefix_logits, prefix_len, config.seed)
         cancelled = False
         queued: list[torch.cuda.Event] = []
+        first, last = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        first.record()
         for i in range(t_max - 1):
             # Observed between steps (ime.py:971-973): the host waits until at
             # most RUN_AHEAD steps are queued, so a cancel stops the group
@@ -618,11 +633,14 @@ class CandidateGroupEngine:
             ev = torch.cuda.Event()
             ev.record()
             queued.append(ev)
+        last.record()
         ids = g.out_ids.cpu()
         cnt = g.counts.cpu().tolist()
         sums = g.logp_sum.cpu().tolist()
         eos = g.eos_hit.cpu().tolist()
         fed = int(g.fed.item())
+        self._replay[0] += first.elapsed_time(last)
+        self._replay[1] += len(queued)
         raw = []
         for i in range(n):
             row = tuple(int(x) for x in ids[i][ids[i] >= 0].tolist())

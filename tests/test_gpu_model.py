@@ -518,6 +518,94 @@ def test_candidate_group_adaptive_refill():
     assert [x.token_ids for x in again.raw_candidates] == [x.token_ids for x in raw]
 
 
+def _record_rounds(eng):
+    """Wrap the round generator: per round, (branches, sampling params, free
+    pages on entry, pages the round allocated, banned sequences)."""
+    rounds = []
+    for name in ("_generate", "_generate_graphed"):
+        inner = getattr(eng, name)
+
+        def wrapped(prefix_logits, page_table, prefix_len, config, cancellation, banned=(),
+                    _inner=inner):
+            free = eng.rt.cache_manager.available_size
+            out = _inner(prefix_logits, page_table, prefix_len, config, cancellation,
+                         banned=banned)
+            rounds.append((config.num_candidates, config.sampling, free,
+                           sum(len(a) for a in out[1]), [tuple(b) for b in banned]))
+            return out
+
+        setattr(eng, name, wrapped)
+    return rounds
+
+
+def test_attnres_0p214b_refill_rounds():
+    """C3's refill leg on the full 32-layer Block-AttnRes model: a greedy
+    first round (top_k 1) leaves one distinct candidate, so sampled refill
+    rounds of 8 x 32 steps follow up to 24 candidates (ime.py:478-600).
+    Every round starts with only the prefix pages held (the previous round's
+    suffix KV was freed, :588-592) and allocates 8 x 31 suffix pages; the
+    rounds follow the refill schedule (temperature 0.75 + 0.10 r, top_k 96 +
+    32 r); round 2's tokens are the sampling oracle's draws from the GPU's
+    logits with the first round's sequence banned; graph-replayed rounds give
+    the eager rounds' candidates; the prefix pages are all that remain."""
+    c = MINIMIND_ATTNRES_0P214B
+    eng, _ = _engine(c, 214)
+    prefix = _prefix(214, 64, c.vocab_size)
+    rec = _record_decode_logits(eng)
+    rounds = _record_rounds(eng)
+    t = 32
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=t, min_new_tokens=2,
+                               sampling=SamplingParams(temperature=0.35, top_k=1, top_p=1.0),
+                               max_candidates=24)
+    res = eng.complete(prefix, cfg)
+    raw = res.raw_candidates
+    total = eng.rt.num_pages
+    assert res.refill_rounds >= 1 and len(rounds) == 1 + res.refill_rounds
+    assert len(raw) == sum(r[0] for r in rounds) <= 24
+    for i, (n, sp, free, alloc, banned) in enumerate(rounds):
+        assert free == total - len(prefix), (i, free)
+        assert alloc == n * (t - 1), (i, alloc)
+        if i:
+            assert n == 8
+            assert sp.temperature == pytest.approx(min(0.95, 0.75 + 0.10 * (i - 1)))
+            assert sp.top_k == min(160, 96 + 32 * (i - 1)) and sp.top_p == 0.95
+            assert banned, "every refill round bans the earlier candidates"
+    assert eng.rt.cache_manager.available_size == total - len(prefix)
+    greedy = raw[0].token_ids
+    assert all(r.token_ids == greedy for r in raw[:8]) and len(greedy) == t
+    sp = rounds[1][1]
+    uni = osamp.stateless_uniforms([cfg.seed + 8 * 100_003 + i for i in range(8)], t)
+    steps = [(list(range(8)), res.prefix_logits.float().cpu().expand(8, -1))] + rec[t - 1: 2 * (t - 1)]
+    checked = 0
+    for j, (rows, lg) in enumerate(steps):
+        assert rows == list(range(8))
+        for r in rows:
+            hist = raw[8 + r].token_ids
+            fb = [greedy[j]] if j >= 2 and hist[:j] == greedy[:j] else []
+            want, _, d = osamp.sample_row(lg[r].numpy(), sp.temperature, sp.top_k, sp.top_p,
+                                          float(uni[r, j]), fb, detail=True)
+            assert hist[j] not in fb
+            if d["u_margin"] > 1e-5 and d["cut_margin"] > 1e-5:
+                assert hist[j] == want, (j, r, hist[j], want)
+                checked += 1
+            else:
+                assert hist[j] in set(d["order"].tolist())
+    assert checked >= 0.9 * 8 * t
+    shown = [x.token_ids for x in res.candidates]
+    assert len(shown) == 3 and len(set(shown)) == 3
+    # graph-replayed rounds on the same runtime: the same candidates
+    eng.reset_prefix_cache()
+    graphed = CandidateGroupEngine(eng.rt, use_graphs=True)
+    g_rounds = _record_rounds(graphed)
+    g = graphed.complete(prefix, cfg)
+    assert g.refill_rounds == res.refill_rounds
+    assert [x.token_ids for x in g.raw_candidates] == [x.token_ids for x in raw]
+    assert [(r[0], r[2], r[3]) for r in g_rounds] == [(r[0], r[2], r[3]) for r in rounds]
+    assert g.replayed_steps == sum(r[0] > 0 for r in g_rounds) * (t - 1)
+    graphed.reset_prefix_cache()
+    assert eng.rt.cache_manager.available_size == total
+
+
 def test_graph_replay_matches_eager_refill():
     """Refill rounds replayed from captured graphs, with the banned-repeat
     rule evaluated on the device, give the eager rounds' candidates."""

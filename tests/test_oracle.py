@@ -650,3 +650,74 @@ def test_sample_ties_take_lower_id_first():
     # three-way tie at the top: top_k 2 keeps ids 1 and 3, in that order
     assert osamp.sample_row(x, 1.0, 2, 1.0, 0.25)[0] == 1
     assert osamp.sample_row(x, 1.0, 2, 1.0, 0.75)[0] == 3
+
+
+from dataclasses import replace  # noqa: E402
+
+from aios_amd.config import ModelConfig  # noqa: E402
+from oracle.cpu_decoder import PagedCpuDecoder  # noqa: E402
+
+
+def _small_cfg(**kw):
+    base = dict(num_layers=2, num_qo_heads=4, num_kv_heads=2, head_dim=16, hidden_size=64,
+                vocab_size=97, intermediate_size=96, rope_theta=10000.0)
+    base.update(kw)
+    return ModelConfig(**base)
+
+
+def test_cpu_decoder_matches_dense_oracle():
+    """The KV-cached CPU decoder (the full-model CPU baseline) in float32:
+    prefix prefill, an LCP extension and three rows of decode steps over
+    scattered pages give the dense oracle's last-position logits; relabelling
+    the pages changes nothing (bitwise)."""
+    from aios_amd.qwen3 import init_weights
+
+    c = _small_cfg()
+    w = init_weights(c, 5, "cpu", std=0.15)
+    om = OracleModel(c, w)
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(c.vocab_size, (9,), generator=g).tolist()
+    conts = torch.randint(c.vocab_size, (3, 3), generator=g)
+
+    def run(perm):
+        dec = PagedCpuDecoder(c, w, torch.float32, num_pages=64)
+        pages = perm[:9]
+        first = dec.prefill(ids[:6], pages)
+        ext = dec.prefill(ids, pages, cached_len=6)
+        rows = [pages.clone() for _ in range(3)]
+        nxt = 9
+        steps = []
+        for s in range(3):
+            new = perm[nxt: nxt + 3]
+            nxt += 3
+            rows = [torch.cat([r, new[i: i + 1]]) for i, r in enumerate(rows)]
+            steps.append(dec.decode(conts[:, s], rows, new))
+        return first, ext, steps
+
+    perm_a = torch.randperm(64, generator=g).to(torch.int32)
+    perm_b = torch.randperm(64, generator=g).to(torch.int32)
+    first, ext, steps = run(perm_a)
+    ref = om.logits(torch.tensor([ids]), 0)[0]
+    assert (first - ref[5]).abs().max() < 1e-4
+    assert (ext - ref[8]).abs().max() < 1e-4
+    for s in range(3):
+        seq = torch.cat([torch.tensor(ids).expand(3, -1), conts[:, : s + 1]], 1)
+        want = om.logits(seq, seq.shape[1] - 1)[:, -1]
+        assert (steps[s] - want).abs().max() < 1e-4, s
+    first_b, ext_b, steps_b = run(perm_b)
+    assert torch.equal(first, first_b) and torch.equal(ext, ext_b)
+    assert all(torch.equal(x, y) for x, y in zip(steps, steps_b))
+
+
+def test_cpu_decoder_bf16_close_to_fp32():
+    from aios_amd.qwen3 import init_weights
+
+    c = _small_cfg(head_dim=32, num_qo_heads=4, num_kv_heads=1, hidden_size=128)
+    w = init_weights(c, 6, "cpu", std=0.1)
+    ids = list(range(3, 20))
+    pages = torch.randperm(32, generator=torch.Generator().manual_seed(6)).to(torch.int32)
+    a = PagedCpuDecoder(c, w, torch.float32, num_pages=32).prefill(ids, pages)
+    b = PagedCpuDecoder(c, w, torch.bfloat16, num_pages=32).prefill(ids, pages)
+    assert (a - b).abs().max() < 0.1 * a.abs().max()
+    with pytest.raises(ValueError, match="standard residual"):
+        PagedCpuDecoder(replace(c, residual_type="block_attnres", attnres_num_blocks=1), w)
