@@ -217,9 +217,14 @@ static int check_plan(const aios_attn_plan_t* p, int phase) {
 }
 
 // The attention kernels address one layer's K (or V) cache with 32-bit byte
-// offsets (buffer descriptors), so a layer's cache must stay below 4 GiB.
+// offsets (buffer descriptors), so a layer's cache must stay below 4 GiB,
+// and form a page's offset with a 24-bit multiply, so the pool holds fewer
+// than 2^24 pages.
 static int check_cache(int64_t kv_num_pages, int64_t tok_stride) {
   if (kv_num_pages < 0) return fail(AIOS_ERR_INVALID, "negative page count");
+  if (kv_num_pages >= (1ll << 24))
+    return fail(AIOS_ERR_UNSUPPORTED, "a pool of %lld pages exceeds the 2^24 - 1 the kernels address",
+                (long long)kv_num_pages);
   const int64_t bytes = kv_num_pages * tok_stride * 2;
   if (bytes > 0xffff0000ll)
     return fail(AIOS_ERR_UNSUPPORTED,

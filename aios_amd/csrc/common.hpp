@@ -83,6 +83,19 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 __device__ __forceinline__ float xrow_max(float x) { return xor32_max(xor16_max(x)); }
+// The cross-row maxima of two values at once, three swaps instead of four:
+// swapping a's odd rows with b's even rows and taking the max leaves
+// pairwise maxima of a in rows 0 and 2 and of b in rows 1 and 3; the
+// half swap completes both (a's in rows 0 and 2, b's in 1 and 3); a last
+// row swap hands every lane both.
+__device__ __forceinline__ void xrow_max2(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const float m = vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const float mm = xor32_max(m);
+  const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(mm), __float_as_uint(mm), false, false);
+  a = __uint_as_float(t[0]);
+  b = __uint_as_float(t[1]);
+}
 __device__ __forceinline__ float xrow_sum(float x) { return xor32_sum(xor16_sum(x)); }
 
 }  // namespace aios

@@ -87,6 +87,15 @@ __device__ __forceinline__ bf16x4 lds_read_tr(const uint8_t* p) {
   asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr) : "memory");
   return __builtin_bit_cast(bf16x4, r);
 }
+// The same read at a compile-time byte offset from a 32-bit LDS address
+// (the instruction's 16-bit offset field, so no address add per read).
+template <uint32_t OFF>
+__device__ __forceinline__ bf16x4 lds_read_tr_at(uint32_t addr) {
+  static_assert(OFF < 65536, "ds offset field");
+  uint64_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return __builtin_bit_cast(bf16x4, r);
+}
 __device__ __forceinline__ void lds_wait_tied(bf16x4& a, bf16x4& b) {
   uint64_t x = __builtin_bit_cast(uint64_t, a), y = __builtin_bit_cast(uint64_t, b);
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x), "+v"(y));
@@ -116,6 +125,10 @@ struct KVTile {
   static __device__ __forceinline__ int v_rot(int t) { return D == 128 ? t : 2 * t; }
   static __device__ __forceinline__ int k_slot(int t, int c) { return (c + k_rot(t)) % CPR; }
   static __device__ __forceinline__ int v_slot(int t, int c) { return (c + v_rot(t)) % CPR; }
+  // Whether token t + 16 keeps token t's rotation (modulo the row), so that
+  // the second 16-token half of a sub-tile is a constant byte offset away.
+  static constexpr bool HALF_SAME = (D == 128 ? 32 : D == 96 ? 8 : 16) % CPR == 0 &&
+                                    (D == 128 ? 16 : 32) % CPR == 0;
   // Inverses: which chunk a slot holds.
   static __device__ __forceinline__ int k_chunk(int t, int slot) {
     return (slot + CPR - k_rot(t) % CPR) % CPR;
@@ -134,6 +147,7 @@ struct TileEngine {
   bf16x8 qf[RT][KSTEPS];
   f32x4 o[RT][DTILES];
   float m_run[RT];
+  float nm[RT];     // -(m_run, or 0 while m_run is -inf): the exponent offset
   float l_run[RT];  // row totals, set by finish()
   f32x4 ol[RT];     // row sums of P by MFMA (every element holds the sum)
   int limit[RT];   // CAUSAL: last visible KV position of the lane's rows
@@ -158,6 +172,7 @@ struct TileEngine {
 #pragma unroll
       for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
       m_run[rt] = kNegInf;
+      nm[rt] = 0.f;
       l_run[rt] = 0.f;
       ol[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -205,6 +220,10 @@ struct TileEngine {
     // scalar registers.
     static_assert(T::SUB_KB % (64 * 16) == 0, "K part of a sub-tile in whole wavefront loads");
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    // When a whole load of the workgroup spans whole rows and the K part of
+    // a sub-tile whole loads, load j's token is load 0's plus a constant.
+    constexpr bool kTokStep = (kEngineThreads * 16) % T::ROWB == 0 &&
+                              T::SUB_KB % (kEngineThreads * 16) == 0;
     int tok_j[T::LPS];
     uint32_t coff_j[T::LPS];
     bool isv_j[T::LPS];
@@ -222,7 +241,9 @@ struct TileEngine {
     // Raw buffer descriptors over this head's K and V rows: the last valid
     // byte is the end of the last page's row, so a page id clamped to
     // num_pages lands past it and the load returns zeros (the hardware range
-    // check); the host keeps a layer's cache below 4 GiB so offsets are 32-bit.
+    // check); the host keeps a layer's cache below 4 GiB so offsets are 32-bit
+    // and the pool below 2^24 pages so a page id times the row stride is one
+    // 24-bit multiply (v_mul_u32_u24, full rate).
     const uint32_t tok_b = (uint32_t)tok_bytes;
     const uint32_t n_pages = (uint32_t)num_pages;
     const int64_t n_rec64 = num_pages > 0 ? (num_pages - 1) * tok_bytes + T::ROWB : 0;
@@ -241,11 +262,20 @@ struct TileEngine {
       // window always covers the sub-tile, lookahead sub-tiles included).
       uint32_t page[T::LPS];
 #pragma unroll
-      for (int j = 0; j < T::LPS; ++j) page[j] = (uint32_t)ids[pos0 + tok_j[j] - win];
+      for (int j = 0; j < T::LPS; ++j) {
+        if constexpr (kTokStep) {
+          // load j serves token tok_j[0] + a compile-time step: one address
+          constexpr int per = kEngineThreads * 16;
+          page[j] = (uint32_t)ids[pos0 + tok_j[0] - win +
+                                  (j * per - (j * per >= T::SUB_KB ? T::SUB_KB : 0)) / T::ROWB];
+        } else {
+          page[j] = (uint32_t)ids[pos0 + tok_j[j] - win];
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < T::LPS; ++j) {
-        const uint32_t off = min(page[j], n_pages) * tok_b + coff_j[j];
+        const uint32_t off = __umul24(min(page[j], n_pages), tok_b) + coff_j[j];
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             isv_j[j] ? rv : rk, (AIOS_LDS void*)(buf + (j * kEngineThreads + wave_u * 64) * 16),
             16, off, 0, 0, 0);
@@ -262,15 +292,16 @@ struct TileEngine {
     for (int s = 0; s < kLookahead; ++s) issue(s);
     wait_vmcnt<(kLookahead - 1) * T::LPS>();
 
+    // Per-lane LDS addresses of the operand reads, relative to ring slot 0.
+    const LaneOff lo = lane_offsets(lds, l16, lg);
+
     // The loop is instantiated twice so that no branch around the math
     // sits inside it: a conditional compute makes the accumulators phi
     // values, and the compiler then copies every O tile once per sub-tile.
     auto loop = [&](auto with_math) {
       for (int it = 0; it < n_sub; ++it) {
         const int pend = min(kLookahead - 1, n_sub - 1 - it);
-        if (pend >= 2)
-          wait_vmcnt<2 * T::LPS>();
-        else if (pend == 1)
+        if (pend >= 1)
           wait_vmcnt<T::LPS>();
         else
           wait_vmcnt<0>();
@@ -285,8 +316,8 @@ struct TileEngine {
           issue(s_next);
         }
         if constexpr (decltype(with_math)::value)
-          compute(lds + (it & (kRing - 1)) * T::SUB_BYTES, kv_begin + it * kSubTok, kv_end,
-                  scale_log2, l16, lg);
+          compute_at(lo, (uint32_t)((it & (kRing - 1)) * T::SUB_BYTES), kv_begin + it * kSubTok,
+                     kv_end, scale_log2, lg);
       }
     };
     if (__builtin_amdgcn_readfirstlane((int)active))
@@ -294,6 +325,73 @@ struct TileEngine {
     else
       loop(std::false_type{});
     finish();
+  }
+
+  // LDS addresses (32-bit, ring slot 0) of the lane's operand reads: K rows
+  // k[tt][s] of read_k and V transpose reads v[tt][dt] of load_v.  With
+  // T::HALF_SAME the second 16-token half is a constant offset from the
+  // first and only [0][.] is kept.
+  struct LaneOff {
+    uint32_t k[T::HALF_SAME ? 1 : 2][KSTEPS];
+    uint32_t v[T::HALF_SAME ? 1 : 2][DTILES];
+  };
+  __device__ __forceinline__ LaneOff lane_offsets(const uint8_t* lds, int l16, int lg) const {
+    LaneOff lo;
+    const uint32_t base = (uint32_t)(uintptr_t)(AIOS_LDS const uint8_t*)lds;
+    constexpr int NH = T::HALF_SAME ? 1 : 2;
+#pragma unroll
+    for (int tt = 0; tt < NH; ++tt) {
+      const int t = tt * 16 + l16;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+        lo.k[tt][s] = base + (uint32_t)(t * T::ROWB + T::k_slot(t, s * 4 + lg) * 16);
+      const int tv = tt * 16 + lg * 4 + (l16 >> 2);
+#pragma unroll
+      for (int dt = 0; dt < DTILES; ++dt) {
+        const int dim = dt * 16 + 4 * (l16 & 3);
+        lo.v[tt][dt] = base + (uint32_t)(T::SUB_KB + tv * T::ROWB +
+                                         T::v_slot(tv, dim >> 3) * 16 + (dim & 7) * 2);
+      }
+    }
+    return lo;
+  }
+
+  // read_k / load_v on the ring slot at byte offset `sb` through the
+  // precomputed addresses: one add per address register and sub-tile, the
+  // second 16-token half (T::HALF_SAME) in the reads' offset field.
+  __device__ __forceinline__ void read_k_at(const LaneOff& lo, uint32_t sb,
+                                            bf16x8 (&kf)[2][KSTEPS]) {
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      const uint32_t a0 = lo.k[0][s] + sb;
+      const uint32_t a1 = T::HALF_SAME ? a0 + 16 * T::ROWB : lo.k[T::HALF_SAME ? 0 : 1][s] + sb;
+      kf[0][s] = *reinterpret_cast<AIOS_LDS const bf16x8*>((AIOS_LDS const uint8_t*)(uintptr_t)a0);
+      kf[1][s] = *reinterpret_cast<AIOS_LDS const bf16x8*>((AIOS_LDS const uint8_t*)(uintptr_t)a1);
+    }
+  }
+  __device__ __forceinline__ void load_v_at(const LaneOff& lo, uint32_t sb,
+                                            bf16x4 (&va)[DTILES][2]) {
+#pragma unroll
+    for (int dt = 0; dt < DTILES; ++dt) {
+      const uint32_t a0 = lo.v[0][dt] + sb;
+      va[dt][0] = lds_read_tr_at<0>(a0);
+      if constexpr (T::HALF_SAME)
+        va[dt][1] = lds_read_tr_at<16 * T::ROWB>(a0);
+      else
+        va[dt][1] = lds_read_tr_at<0>(lo.v[T::HALF_SAME ? 0 : 1][dt] + sb);
+    }
+  }
+  __device__ __forceinline__ void compute_at(const LaneOff& lo, uint32_t sb, int kv0, int kv_end,
+                                             float scale_log2, int lg) {
+    bf16x8 kf[2][KSTEPS];
+    bf16x4 va[DTILES][2];
+    f32x4 st[RT][2];
+    bf16x8 pb[RT];
+    read_k_at(lo, sb, kf);
+    load_v_at(lo, sb, va);
+    mma_s(kf, st);
+    softmax(st, kv0, kv_end, scale_log2, lg, pb);
+    accumulate(va, pb, kv_end - kv0, lg);
   }
 
   // Row totals (after the last compute).
@@ -387,9 +485,15 @@ struct TileEngine {
     }
     bool need[RT];
     bool any = false;
+    if constexpr (RT == 2) {
+      xrow_max2(mx[0], mx[1]);
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) mx[rt] = xrow_max(mx[rt]);
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      mx[rt] = xrow_max(mx[rt]) * scale_log2;
+      mx[rt] *= scale_log2;
       need[rt] = mx[rt] > m_run[rt] + kRescaleSlack;
       any = any || need[rt];
     }
@@ -403,14 +507,14 @@ struct TileEngine {
 #pragma unroll
         for (int dt = 0; dt < DTILES; ++dt) o[rt][dt] *= al;
         m_run[rt] = need[rt] ? mx[rt] : m_run[rt];
+        nm[rt] = need[rt] ? -mx[rt] : nm[rt];
       }
     }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const float m_use = (m_run[rt] == kNegInf) ? 0.f : m_run[rt];
       float p[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) p[j] = fast_exp2(fmaf(x[rt][j], scale_log2, -m_use));
+      for (int j = 0; j < 8; ++j) p[j] = fast_exp2(fmaf(x[rt][j], scale_log2, nm[rt]));
       pb[rt] = __builtin_bit_cast(
           bf16x8, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
                              pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])));

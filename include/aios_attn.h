@@ -158,7 +158,8 @@ int aios_attn_plan(int32_t phase, const int32_t* cu_q_host,
  * cu_q, cu_k and indices are device int32.  A page id outside
  * [0, kv_num_pages) is read as an all-zero K/V row (never dereferenced).
  * One layer's cache (kv_num_pages * Hkv * D * 2 bytes) must be below 4 GiB
- * (the kernels use 32-bit byte offsets); AIOS_ERR_UNSUPPORTED otherwise.
+ * (the kernels use 32-bit byte offsets) and kv_num_pages below 2^24 (a
+ * 24-bit page multiply); AIOS_ERR_UNSUPPORTED otherwise.
  */
 int aios_attn_prefill(const aios_attn_plan_t* plan, const void* q,
                       int64_t q_tok_stride, const void* k_cache,

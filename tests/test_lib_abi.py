@@ -130,3 +130,18 @@ def test_noalloc_limit_matches_header():
     text = HEADER.read_text()
     m = re.search(r"#define AIOS_DECODE_NOALLOC_MAX_BYTES \((\d+)ll << (\d+)\)", text)
     assert m and int(m.group(1)) << int(m.group(2)) == _lib.DECODE_NOALLOC_MAX_BYTES
+
+
+def test_pool_of_2_24_pages_is_rejected():
+    """A page's byte offset is a 24-bit multiply in the kernels: a pool of
+    2^24 pages (here a 2 GiB cache, inside the 4 GiB offset range) is refused
+    before any launch, as is a 4 GiB cache."""
+    lib = _lib.lib()
+    rc, p = _plan(_lib.PHASE_DECODE, [0, 1], [0, 5], hq=4, hkv=1, d=64)
+    assert rc == 0 and p.ws_bytes == 0
+    fake = 1 << 20  # 16-byte aligned, never dereferenced: the call is refused first
+    for pages, what in (((1 << 24), b"2^24"), ((1 << 32) // 128 + 1, b"2^24")):
+        rc = lib.aios_attn_decode(p, fake, 4 * 64, fake, fake, pages, fake, fake, fake, None, 0,
+                                  0.125, None)
+        assert rc == _lib.AIOS_ERR_UNSUPPORTED
+        assert what in lib.aios_last_error()
