@@ -56,4 +56,10 @@ Modules and what pins each function (the checks live in tests/test_oracle.py):
                 The Block-AttnRes trunk composition has no independent
                 implementation or reference-held fixture offline: "parity
                 unpinned" (only its mixer, attnres.py above, is pinned).
+  cpu_decoder.py  KV-cached CPU decoder over the paged pool (the same
+                forward, attention by sdpa_cpu.py), bf16 or fp32: the
+                full-model leg of bench.py's CPU baseline.  Pinned against
+                model.py (float32: prefix prefill, LCP extension and decode
+                steps over scattered pages equal the dense recomputation's
+                logits within 1e-4; a page relabelling changes nothing).
 """
