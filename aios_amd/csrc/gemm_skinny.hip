@@ -87,6 +87,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
     // terms (kept as the bf16 operands; their fp32 sum is exact).
     constexpr int SMAX = kNormMaxFrags / MT;
     bf16x8 hf[SMAX][MT], rf[SMAX][MT];
+    bf16x8 nw[SMAX];  // the norm weight of the quarter, loaded with the rest
     bf16x8 wa[NP][kGemmBatch];
 #pragma unroll
     for (int p = 0; p < NP; ++p)
@@ -99,6 +100,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
 #pragma unroll
     for (int s = 0; s < SMAX; ++s) {
       if (s < steps) {
+        nw[s] = *reinterpret_cast<const bf16x8*>(a.norm_w + k_begin + s * 32);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           hf[s][mt] = xok[mt] ? *reinterpret_cast<const bf16x8*>(a.x + xoff[mt] + s * 32)
@@ -161,7 +163,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
         const int s = s0 + u;
         if (s < steps && s < SMAX) {
           float w8[8];
-          unpack8(*reinterpret_cast<const bf16x8*>(a.norm_w + k_begin + s * 32), w8);
+          unpack8(nw[s], w8);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             float h8[8], r8[8], x8[8];
