@@ -2,10 +2,11 @@
 // per-row ragged suffix (kernel (d)) and the log-sum-exp combine.
 //
 // decode_main_kernel is one launch with two kinds of workgroups:
-//   * prefix workgroups (blockIdx.x < prefix_wgs): the MFMA tile engine over
-//     one chunk of the shared prefix for one kv-head and up to 128 of the
-//     batch*G query rows; the prefix KV is therefore read once per kv-head
-//     for the whole group, not once per candidate;
+//   * prefix workgroups (blockIdx.x < prefix_wgs): the 32-row MFMA tile
+//     engine (TileEngine32) over one chunk of the shared prefix for one
+//     kv-head and up to 128 of the batch*G query rows; the prefix KV is
+//     therefore read once per kv-head for the whole group, not once per
+//     candidate;
 //   * suffix workgroups: one (row, kv-head, split) item of the row's own
 //     pages after the prefix.  Its four wavefronts take the item's
 //     32-position sub-tiles round-robin, gather each into their own LDS
@@ -32,8 +33,7 @@ template <int D>
 __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArgs& a, int wg) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int l16 = lane & 15;
-  const int lg = lane >> 4;
+  const int hl = lane >> 5;
   const int G = a.group;
   const int mg = wg % a.m_groups;
   const int unit = wg / a.m_groups;
@@ -44,20 +44,14 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
   const int h = unit % a.num_kv_heads;
   const int chunk = unit / a.num_kv_heads;
 
-  TileEngine<D, false> eng;
+  TileEngine32<D, false> eng;
   eng.min_limit = 0x7fffffff;
-  int rows[2];
-  bool ok[2];
-  const bf16* qr[2];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int m = mg * 128 + wave * 32 + rt * 16 + l16;
-    rows[rt] = m;
-    ok[rt] = m < a.m_rows;
-    const int b = m / G;
-    const int g = m - b * G;
-    qr[rt] = a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + g) * D;
-  }
+  // The lane's query row (lanes l and l ^ 32 share it).
+  const int m = mg * 128 + wave * 32 + (lane & 31);
+  const bool ok = m < a.m_rows;
+  const int b = m / G;
+  const int g = m - b * G;
+  const bf16* qr = a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + g) * D;
   const int kv_begin = chunk * a.chunk_len;
   const int kv_end = min(a.prefix_len, kv_begin + a.chunk_len);
   const int64_t tok_bytes = a.kv_tok_stride * 2;
@@ -66,29 +60,26 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
   eng.run(lds, reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2,
           reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2, tok_bytes,
           a.num_pages, a.indices, kv_begin, kv_end, a.scale_log2,
-          [&] { eng.load_q(qr[0], ok[0], qr[1], ok[1]); }, active);
+          [&] { eng.load_q(qr, ok); }, active);
 
-  constexpr int DT = D / 16;
+  if (!ok) return;
+  const float l_tot = eng.l_run;
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  // o[nt] register 4j + i: dim 32 nt + 8j + 4h + i of the lane's row; four
+  // consecutive dims stay inside one 16-dim tile of the parts layout.
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const float l_tot = eng.l_run[rt];
-    if (!ok[rt]) continue;
-    const int m = rows[rt];
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    // One store per accumulator tile: 16 rows x 16 dims, 512 contiguous bytes.
+  for (int nt = 0; nt < D / 32; ++nt)
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const f32x4 v = eng.o[rt][dt] * inv;
+    for (int j = 0; j < 4; ++j) {
       uint2 packed;
-      packed.x = pack_bf16x2(v[0], v[1]);
-      packed.y = pack_bf16x2(v[2], v[3]);
-      *reinterpret_cast<uint2*>(a.parts.o + a.parts.o_index(D, h, chunk, m, dt * 16 + lg * 4)) =
+      packed.x = pack_bf16x2(eng.o[nt][4 * j] * inv, eng.o[nt][4 * j + 1] * inv);
+      packed.y = pack_bf16x2(eng.o[nt][4 * j + 2] * inv, eng.o[nt][4 * j + 3] * inv);
+      *reinterpret_cast<uint2*>(a.parts.o + a.parts.o_index(D, h, chunk, m, nt * 32 + 8 * j + 4 * hl)) =
           packed;
     }
-    if (lg == 0)
-      a.parts.lse[a.parts.lse_index(h, chunk, m)] =
-          l_tot > 0.f ? eng.m_run[rt] + fast_log2(l_tot) : kNegInf;
-  }
+  if (hl == 0)
+    a.parts.lse[a.parts.lse_index(h, chunk, m)] =
+        l_tot > 0.f ? eng.m_run + fast_log2(l_tot) : kNegInf;
 }
 
 // ---------------------------------------------------------------------------

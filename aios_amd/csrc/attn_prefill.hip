@@ -17,8 +17,6 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
   __shared__ __align__(16) uint8_t lds[KVTile<D>::LDS_BYTES];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int l16 = lane & 15;
-  const int lg = lane >> 4;
   const int G = a.group;
   // One flat grid: consecutive workgroups take consecutive kv-heads (the
   // hardware deals workgroups round-robin to the XCDs, so with 8 kv-heads
@@ -39,46 +37,39 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
   const int cached = kv_len - q_len;
   const int q_hi = min(q_len, (qt + 1) * a.q_tile);
 
-  TileEngine<D, true> eng;
-  bool ok[2];
-  int64_t out_off[2];
-  const bf16* qr[2];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int m = wave * 32 + rt * 16 + l16;
-    const int i = qt * a.q_tile + m / G;
-    const int g = m - (m / G) * G;
-    ok[rt] = (m < a.q_tile * G) && (i < q_len);
-    qr[rt] = a.q + (int64_t)(q_start + i) * a.q_tok_stride + (int64_t)(h * G + g) * D;
-    out_off[rt] = ((int64_t)(q_start + i) * a.num_qo_heads + (h * G + g)) * D;
-    eng.limit[rt] = cached + i;
-  }
+  TileEngine32<D, true> eng;
+  // The lane's query row (lanes l and l ^ 32 share it).
+  const int m = wave * 32 + (lane & 31);
+  const int i = qt * a.q_tile + m / G;
+  const int g = m - (m / G) * G;
+  const bool ok = (m < a.q_tile * G) && (i < q_len);
+  const bf16* qr = a.q + (int64_t)(q_start + i) * a.q_tok_stride + (int64_t)(h * G + g) * D;
+  const int64_t out_off = ((int64_t)(q_start + i) * a.num_qo_heads + (h * G + g)) * D;
+  eng.limit = cached + i;
   eng.min_limit = cached + qt * a.q_tile;
   // A wavefront whose 32 rows are all past the tile's tokens only helps
   // stream K/V; it skips the math.
-  const int m0 = (threadIdx.x >> 6) * 32;
+  const int m0 = wave * 32;
   const bool active = m0 < a.q_tile * G && qt * a.q_tile + m0 / G < q_len;
   eng.run(lds, reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2,
           reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2, a.kv_tok_stride * 2,
           a.num_pages, a.indices + kv_base, 0, min(kv_len, cached + q_hi), a.scale_log2,
-          [&] { eng.load_q(qr[0], ok[0], qr[1], ok[1]); }, active);
+          [&] { eng.load_q(qr, ok); }, active);
 
-  constexpr int DT = D / 16;
+  if (!ok) return;
+  const float l_tot = eng.l_run;
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  bf16* po = a.out + out_off + 4 * (lane >> 5);
+  // o[nt] register 4j + i: dim 32 nt + 8j + 4h + i of the lane's row
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const float l_tot = eng.l_run[rt];
-    if (!ok[rt]) continue;
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    bf16* po = a.out + out_off[rt];
+  for (int nt = 0; nt < D / 32; ++nt)
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const f32x4 v = eng.o[rt][dt] * inv;
+    for (int j = 0; j < 4; ++j) {
       uint2 packed;
-      packed.x = pack_bf16x2(v[0], v[1]);
-      packed.y = pack_bf16x2(v[2], v[3]);
-      *reinterpret_cast<uint2*>(po + dt * 16 + lg * 4) = packed;
+      packed.x = pack_bf16x2(eng.o[nt][4 * j] * inv, eng.o[nt][4 * j + 1] * inv);
+      packed.y = pack_bf16x2(eng.o[nt][4 * j + 2] * inv, eng.o[nt][4 * j + 3] * inv);
+      *reinterpret_cast<uint2*>(po + nt * 32 + 8 * j) = packed;
     }
-  }
 }
 
 hipError_t launch_prefill(int D, int NW, const PrefillArgs& a, int q_tiles, int batch,

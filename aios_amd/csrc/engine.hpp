@@ -1,34 +1,34 @@
-// MFMA attention tile engine for gfx950, shared by the shared-prefix cascade
-// decode (kernel (c)) and the varlen causal prefill (kernel (b)).
+// MFMA attention tile engines for gfx950, shared by the shared-prefix cascade
+// decode (kernel (c)), the varlen causal prefill (kernel (b)) and the
+// per-row suffix items (kernel (d)).
 //
 // A 256-thread workgroup (4 wavefronts) owns one kv-head, one KV position
-// range and up to 128 query rows (each wavefront 32 rows: two 16-row MFMA
-// tiles).  A query row is any (token or candidate, q-head) pair of the GQA
-// group, so all query heads sharing a kv-head share one K/V stream.
+// range and up to 128 query rows (32 per wavefront).  A query row is any
+// (token or candidate, q-head) pair of the GQA group, so all query heads
+// sharing a kv-head share one K/V stream.
 //
-// Data movement: the range's page ids are staged in LDS, then K/V rows are
-// gathered page by page straight from HBM into an LDS ring of four 32-token
-// sub-tiles with raw-buffer LDS loads (buffer_load_dwordx4 ... lds, no VGPR
-// staging), two sub-tiles ahead of the one being consumed (three measured
-// no faster: the decode launch is not bound by the stream depth, and a
-// shallower queue lets the suffix items' dependent loads through sooner).  Rows are
-// stored token-major with the sixteen-byte chunks of each row rotated by a
-// multiple of the token index (chosen per head size, see KVTile) so that
-// the MFMA operand reads below avoid LDS bank conflicts.  Masked or
-// out-of-range positions load a zero row.
+// Data movement (stream_kv): the range's page ids are staged in LDS, then
+// K/V rows are gathered page by page straight from HBM into an LDS ring of
+// four 32-token sub-tiles with raw-buffer LDS loads (buffer_load_dwordx4
+// ... lds, no VGPR staging), two sub-tiles ahead of the one being consumed
+// (three measured no faster).  Rows are stored token-major with the
+// sixteen-byte chunks of each row rotated by a multiple of the token index
+// (chosen per head size and engine, see KVTile) so that the MFMA operand
+// reads avoid LDS bank conflicts.  Masked or out-of-range positions load a
+// zero row.
 //
-// Math per 32-token sub-tile and wavefront:
-//   S^T = K Q^T         v_mfma_f32_16x16x32_bf16, A = K rows (ds_read_b128),
+// Math per 32-token sub-tile and wavefront (TileEngine32, the ring path):
+//   S^T = K Q^T         v_mfma_f32_32x32x16_bf16, A = K rows (ds_read_b128),
 //                       B = Q fragments kept in registers
-//   online softmax      one query row per lane column; row max over the four
-//                       lane groups by v_permlane16/32_swap; log2 domain; the
-//                       reference max moves only when a row's max grows by
-//                       more than 2^8, so O is rarely rescaled
+//   online softmax      one query row per lane pair (l, l ^ 32); row max of
+//                       16 scores in the lane plus v_permlane32_swap; log2
+//                       domain; the reference max moves only when a row's max
+//                       grows by more than 2^8, so O is rarely rescaled
 //   O^T += V^T P^T      A = V^T read with ds_read_b64_tr_b16 (the LDS
 //                       transpose read) from the token-major V rows, B = P^T,
-//                       which is exactly the fragment each lane holds after
-//                       the S^T step (tokens {4g..4g+3} and {16+4g..16+4g+3}
-//                       of lane group g)
+//                       the fragment each lane holds after the S^T step
+// TileEngine is the same math with 16 x 16 x 32 MFMA tiles, used with one
+// 16-row tile by the suffix items (G <= 16 live rows).
 // This is the offset-causal GQA softmax attention of
 // python/aios/attention/flashinfer.py:33-91 (decode: q_len 1).
 #pragma once
@@ -103,7 +103,9 @@ __device__ __forceinline__ void lds_wait_tied(bf16x4& a, bf16x4& b) {
   b = __builtin_bit_cast(bf16x4, y);
 }
 
-template <int D>
+// W32: the layout read by TileEngine32 (32 x 32 MFMA tiles); otherwise the
+// one read by TileEngine (16 x 16 tiles).  The gathers write either.
+template <int D, bool W32 = false>
 struct KVTile {
   static constexpr int ROWB = 2 * D;                 // bytes of one K or V row
   static constexpr int CPR = D / 8;                  // 16-byte chunks per row
@@ -119,16 +121,23 @@ struct KVTile {
   // wavefronts, the exact lane patterns of the reads below): K (read with
   // ds_read_b128) conflict-free for D = 64 and 128 and at the best measured
   // rate for D = 96; V (read with ds_read_b64_tr_b16) conflict-free.
+  // W32 (derived for 64 banks of 4 bytes, a 16-lane quarter of a
+  // ds_read_b128 and a 32-lane half of a ds_read_b64_tr_b16 conflict-free):
+  // K lanes t = 0..15 of one chunk column hit 16 distinct 16-byte bank
+  // groups (D = 128: rotation t; D = 96: t / 4 against the 48-dword row
+  // pitch; D = 64: t / 2 with two rows per bank period); V: the 4 tokens x 4
+  // chunks of a half-read land in distinct groups (D = 128: 4t; D = 64:
+  // 4 (t / 2); D = 96: none needed), and token t + 8 keeps token t's slot.
   static __device__ __forceinline__ int k_rot(int t) {
-    return D == 128 ? 2 * t : D == 96 ? t >> 1 : t;
+    if constexpr (W32) return D == 128 ? t : D == 96 ? t >> 2 : t >> 1;
+    else return D == 128 ? 2 * t : D == 96 ? t >> 1 : t;
   }
-  static __device__ __forceinline__ int v_rot(int t) { return D == 128 ? t : 2 * t; }
+  static __device__ __forceinline__ int v_rot(int t) {
+    if constexpr (W32) return D == 128 ? 4 * t : D == 96 ? 0 : 4 * (t >> 1);
+    else return D == 128 ? t : 2 * t;
+  }
   static __device__ __forceinline__ int k_slot(int t, int c) { return (c + k_rot(t)) % CPR; }
   static __device__ __forceinline__ int v_slot(int t, int c) { return (c + v_rot(t)) % CPR; }
-  // Whether token t + 16 keeps token t's rotation (modulo the row), so that
-  // the second 16-token half of a sub-tile is a constant byte offset away.
-  static constexpr bool HALF_SAME = (D == 128 ? 32 : D == 96 ? 8 : 16) % CPR == 0 &&
-                                    (D == 128 ? 16 : 32) % CPR == 0;
   // Inverses: which chunk a slot holds.
   static __device__ __forceinline__ int k_chunk(int t, int slot) {
     return (slot + CPR - k_rot(t) % CPR) % CPR;
@@ -137,6 +146,148 @@ struct KVTile {
     return (slot + CPR - v_rot(t) % CPR) % CPR;
   }
 };
+
+// Streams KV positions [kv_begin, kv_end) of one kv-head (kc / vc point at
+// head h of page 0; tok_bytes = page stride) whose page ids are
+// idx[kv_begin .. kv_end) through the LDS ring (layout T) with all
+// kEngineThreads threads of the workgroup; `qload()` issues the Q loads,
+// `math(sb, kv0)` runs one sub-tile's math (ring slot at byte offset sb,
+// positions kv0 ..) and is skipped when `active` is false (a wavefront whose
+// rows are all padding only helps stream).
+template <class T, typename QLoad, typename Math>
+__device__ __forceinline__ void stream_kv(uint8_t* lds, const uint8_t* kc, const uint8_t* vc,
+                                          int64_t tok_bytes, int64_t num_pages, const int32_t* idx,
+                                          int kv_begin, int kv_end, QLoad&& qload, Math&& math,
+                                          bool active) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int n_sub = (kv_end - kv_begin + kSubTok - 1) / kSubTok;
+  if (n_sub <= 0) return;
+
+  int32_t* ids = reinterpret_cast<int32_t*>(lds + T::RING_BYTES);
+  int win = kv_begin;
+  auto stage_ids = [&]() {
+    for (int i = tid; i < kIdWindow; i += kEngineThreads) {
+      const int p = win + i;
+      ids[i] = p < kv_end ? idx[p] : -1;
+    }
+  };
+  stage_ids();
+  lds_barrier();
+  // Q is needed only at the first compute: its loads go out after the page
+  // ids (which gate every DMA) and ahead of the DMAs, so the first wait
+  // below covers them.
+  qload();
+
+  // Loop-invariant part of every DMA load of this thread: which token of
+  // the sub-tile it serves, and the byte offset (rotated chunk) inside that
+  // token's K or V row.  Whether load j of a wavefront fills K or V rows is
+  // uniform over the wavefront (the K part of a sub-tile is a whole number
+  // of 1 KiB wavefront loads), so it selects a buffer descriptor held in
+  // scalar registers.
+  static_assert(T::SUB_KB % (64 * 16) == 0, "K part of a sub-tile in whole wavefront loads");
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  // When a whole load of the workgroup spans whole rows and the K part of
+  // a sub-tile whole loads, load j's token is load 0's plus a constant.
+  constexpr bool kTokStep = (kEngineThreads * 16) % T::ROWB == 0 &&
+                            T::SUB_KB % (kEngineThreads * 16) == 0;
+  int tok_j[T::LPS];
+  uint32_t coff_j[T::LPS];
+  bool isv_j[T::LPS];
+#pragma unroll
+  for (int j = 0; j < T::LPS; ++j) {
+    const bool isv = (j * kEngineThreads + wave_u * 64) * 16 >= T::SUB_KB;
+    const int off = (j * kEngineThreads + tid) * 16;
+    const int o2 = isv ? off - T::SUB_KB : off;
+    const int t = o2 / T::ROWB;
+    const int slot = (o2 - t * T::ROWB) >> 4;
+    tok_j[j] = t;
+    isv_j[j] = isv;
+    coff_j[j] = (uint32_t)((isv ? T::v_chunk(t, slot) : T::k_chunk(t, slot)) * 16);
+  }
+  // Raw buffer descriptors over this head's K and V rows: the last valid
+  // byte is the end of the last page's row, so a page id clamped to
+  // num_pages lands past it and the load returns zeros (the hardware range
+  // check); the host keeps a layer's cache below 4 GiB so offsets are 32-bit
+  // and the pool below 2^24 pages so a page id times the row stride is one
+  // 24-bit multiply (v_mul_u32_u24, full rate).
+  const uint32_t tok_b = (uint32_t)tok_bytes;
+  const uint32_t n_pages = (uint32_t)num_pages;
+  const int64_t n_rec64 = num_pages > 0 ? (num_pages - 1) * tok_bytes + T::ROWB : 0;
+  const int n_rec = (int)(n_rec64 < 0xffffffffll ? n_rec64 : 0xffffffffll);
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kc, (short)0, n_rec, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vc, (short)0, n_rec, kBufferWord3);
+  auto issue = [&](int s) {
+    uint8_t* buf = lds + (s & (kRing - 1)) * T::SUB_BYTES;
+    const int pos0 = kv_begin + s * kSubTok;
+    // All page-id reads first: every LDS DMA rewrites M0, which waits for
+    // outstanding LDS instructions, so reads interleaved with the DMAs
+    // would each pay a full LDS round trip.
+    // Positions past kv_end read the -1 that stage_ids left there (the
+    // window always covers the sub-tile, lookahead sub-tiles included).
+    uint32_t page[T::LPS];
+#pragma unroll
+    for (int j = 0; j < T::LPS; ++j) {
+      if constexpr (kTokStep) {
+        // load j serves token tok_j[0] + a compile-time step: one address
+        constexpr int per = kEngineThreads * 16;
+        page[j] = (uint32_t)ids[pos0 + tok_j[0] - win +
+                                (j * per - (j * per >= T::SUB_KB ? T::SUB_KB : 0)) / T::ROWB];
+      } else {
+        page[j] = (uint32_t)ids[pos0 + tok_j[j] - win];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < T::LPS; ++j) {
+      const uint32_t off = __umul24(min(page[j], n_pages), tok_b) + coff_j[j];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          isv_j[j] ? rv : rk, (AIOS_LDS void*)(buf + (j * kEngineThreads + wave_u * 64) * 16),
+          16, off, 0, 0, 0);
+    }
+  };
+
+  // The lookahead sub-tiles are issued unconditionally (those past the
+  // range gather the zero row into ring slots nobody reads), so one wait
+  // with a fixed count covers the Q loads and sub-tile 0 on every path.
+  // The compiler then sees Q complete before the loop; with Q possibly
+  // still in flight it would wait for every outstanding DMA (vmcnt(0))
+  // before each sub-tile's first MFMA and serialise the ring.
+#pragma unroll
+  for (int s = 0; s < kLookahead; ++s) issue(s);
+  wait_vmcnt<(kLookahead - 1) * T::LPS>();
+
+  // The loop is instantiated twice so that no branch around the math
+  // sits inside it: a conditional compute makes the accumulators phi
+  // values, and the compiler then copies every O tile once per sub-tile.
+  auto loop = [&](auto with_math) {
+    for (int it = 0; it < n_sub; ++it) {
+      const int pend = min(kLookahead - 1, n_sub - 1 - it);
+      if (pend >= 1)
+        wait_vmcnt<T::LPS>();
+      else
+        wait_vmcnt<0>();
+      lds_barrier();  // sub-tile `it` is in LDS; every wave is done with it-1
+      const int s_next = it + kLookahead;
+      if (s_next < n_sub) {
+        if (kv_begin + s_next * kSubTok >= win + kIdWindow) {
+          win += kIdWindow;
+          stage_ids();
+          lds_barrier();
+        }
+        issue(s_next);
+      }
+      if constexpr (decltype(with_math)::value)
+        math((uint32_t)((it & (kRing - 1)) * T::SUB_BYTES), kv_begin + it * kSubTok);
+    }
+  };
+  if (__builtin_amdgcn_readfirstlane((int)active))
+    loop(std::true_type{});
+  else
+    loop(std::false_type{});
+}
 
 template <int D, bool CAUSAL, int RT = 2>
 struct TileEngine {
@@ -160,11 +311,6 @@ struct TileEngine {
     for (int s = 0; s < KSTEPS; ++s)
       qf[rt][s] = ok ? *reinterpret_cast<const bf16x8*>(q + s * 32 + lg * 8) : bf16x8{};
   }
-  __device__ __forceinline__ void load_q(const bf16* q0, bool ok0, const bf16* q1, bool ok1) {
-    static_assert(RT == 2, "two row tiles");
-    load_q_tile(0, q0, ok0);
-    load_q_tile(1, q1, ok1);
-  }
 
   __device__ __forceinline__ void reset() {
 #pragma unroll
@@ -176,222 +322,6 @@ struct TileEngine {
       l_run[rt] = 0.f;
       ol[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-  }
-
-  // Stream KV positions [kv_begin, kv_end) of one kv-head (kc / vc point at
-  // head h of page 0; tok_bytes = page stride) whose page ids are
-  // idx[kv_begin .. kv_end), with all kEngineThreads threads of the
-  // workgroup.  `qload` loads the Q fragment; an inactive wavefront (all of
-  // its rows padding) streams K/V but skips the math.  Leaves o
-  // (unnormalised), m_run and the row total l_run.
-  template <typename QLoad>
-  __device__ void run(uint8_t* lds, const uint8_t* kc, const uint8_t* vc, int64_t tok_bytes,
-                      int64_t num_pages, const int32_t* idx, int kv_begin, int kv_end,
-                      float scale_log2, QLoad&& qload, bool active = true) {
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int l16 = lane & 15;
-    const int lg = lane >> 4;
-    reset();
-    const int n_sub = (kv_end - kv_begin + kSubTok - 1) / kSubTok;
-    if (n_sub <= 0) return;
-
-    int32_t* ids = reinterpret_cast<int32_t*>(lds + T::RING_BYTES);
-    int win = kv_begin;
-    auto stage_ids = [&]() {
-      for (int i = tid; i < kIdWindow; i += kEngineThreads) {
-        const int p = win + i;
-        ids[i] = p < kv_end ? idx[p] : -1;
-      }
-    };
-    stage_ids();
-    lds_barrier();
-    // Q is needed only at the first compute: its loads go out after the page
-    // ids (which gate every DMA) and ahead of the DMAs, so the first wait
-    // below covers them.
-    qload();
-
-    // Loop-invariant part of every DMA load of this thread: which token of
-    // the sub-tile it serves, and the byte offset (rotated chunk) inside that
-    // token's K or V row.  Whether load j of a wavefront fills K or V rows is
-    // uniform over the wavefront (the K part of a sub-tile is a whole number
-    // of 1 KiB wavefront loads), so it selects a buffer descriptor held in
-    // scalar registers.
-    static_assert(T::SUB_KB % (64 * 16) == 0, "K part of a sub-tile in whole wavefront loads");
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    // When a whole load of the workgroup spans whole rows and the K part of
-    // a sub-tile whole loads, load j's token is load 0's plus a constant.
-    constexpr bool kTokStep = (kEngineThreads * 16) % T::ROWB == 0 &&
-                              T::SUB_KB % (kEngineThreads * 16) == 0;
-    int tok_j[T::LPS];
-    uint32_t coff_j[T::LPS];
-    bool isv_j[T::LPS];
-#pragma unroll
-    for (int j = 0; j < T::LPS; ++j) {
-      const bool isv = (j * kEngineThreads + wave_u * 64) * 16 >= T::SUB_KB;
-      const int off = (j * kEngineThreads + tid) * 16;
-      const int o2 = isv ? off - T::SUB_KB : off;
-      const int t = o2 / T::ROWB;
-      const int slot = (o2 - t * T::ROWB) >> 4;
-      tok_j[j] = t;
-      isv_j[j] = isv;
-      coff_j[j] = (uint32_t)((isv ? T::v_chunk(t, slot) : T::k_chunk(t, slot)) * 16);
-    }
-    // Raw buffer descriptors over this head's K and V rows: the last valid
-    // byte is the end of the last page's row, so a page id clamped to
-    // num_pages lands past it and the load returns zeros (the hardware range
-    // check); the host keeps a layer's cache below 4 GiB so offsets are 32-bit
-    // and the pool below 2^24 pages so a page id times the row stride is one
-    // 24-bit multiply (v_mul_u32_u24, full rate).
-    const uint32_t tok_b = (uint32_t)tok_bytes;
-    const uint32_t n_pages = (uint32_t)num_pages;
-    const int64_t n_rec64 = num_pages > 0 ? (num_pages - 1) * tok_bytes + T::ROWB : 0;
-    const int n_rec = (int)(n_rec64 < 0xffffffffll ? n_rec64 : 0xffffffffll);
-    const __amdgpu_buffer_rsrc_t rk =
-        __builtin_amdgcn_make_buffer_rsrc((void*)kc, (short)0, n_rec, kBufferWord3);
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc((void*)vc, (short)0, n_rec, kBufferWord3);
-    auto issue = [&](int s) {
-      uint8_t* buf = lds + (s & (kRing - 1)) * T::SUB_BYTES;
-      const int pos0 = kv_begin + s * kSubTok;
-      // All page-id reads first: every LDS DMA rewrites M0, which waits for
-      // outstanding LDS instructions, so reads interleaved with the DMAs
-      // would each pay a full LDS round trip.
-      // Positions past kv_end read the -1 that stage_ids left there (the
-      // window always covers the sub-tile, lookahead sub-tiles included).
-      uint32_t page[T::LPS];
-#pragma unroll
-      for (int j = 0; j < T::LPS; ++j) {
-        if constexpr (kTokStep) {
-          // load j serves token tok_j[0] + a compile-time step: one address
-          constexpr int per = kEngineThreads * 16;
-          page[j] = (uint32_t)ids[pos0 + tok_j[0] - win +
-                                  (j * per - (j * per >= T::SUB_KB ? T::SUB_KB : 0)) / T::ROWB];
-        } else {
-          page[j] = (uint32_t)ids[pos0 + tok_j[j] - win];
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int j = 0; j < T::LPS; ++j) {
-        const uint32_t off = __umul24(min(page[j], n_pages), tok_b) + coff_j[j];
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            isv_j[j] ? rv : rk, (AIOS_LDS void*)(buf + (j * kEngineThreads + wave_u * 64) * 16),
-            16, off, 0, 0, 0);
-      }
-    };
-
-    // The lookahead sub-tiles are issued unconditionally (those past the
-    // range gather the zero row into ring slots nobody reads), so one wait
-    // with a fixed count covers the Q loads and sub-tile 0 on every path.
-    // The compiler then sees Q complete before the loop; with Q possibly
-    // still in flight it would wait for every outstanding DMA (vmcnt(0))
-    // before each sub-tile's first MFMA and serialise the ring.
-#pragma unroll
-    for (int s = 0; s < kLookahead; ++s) issue(s);
-    wait_vmcnt<(kLookahead - 1) * T::LPS>();
-
-    // Per-lane LDS addresses of the operand reads, relative to ring slot 0.
-    const LaneOff lo = lane_offsets(lds, l16, lg);
-
-    // The loop is instantiated twice so that no branch around the math
-    // sits inside it: a conditional compute makes the accumulators phi
-    // values, and the compiler then copies every O tile once per sub-tile.
-    auto loop = [&](auto with_math) {
-      for (int it = 0; it < n_sub; ++it) {
-        const int pend = min(kLookahead - 1, n_sub - 1 - it);
-        if (pend >= 1)
-          wait_vmcnt<T::LPS>();
-        else
-          wait_vmcnt<0>();
-        lds_barrier();  // sub-tile `it` is in LDS; every wave is done with it-1
-        const int s_next = it + kLookahead;
-        if (s_next < n_sub) {
-          if (kv_begin + s_next * kSubTok >= win + kIdWindow) {
-            win += kIdWindow;
-            stage_ids();
-            lds_barrier();
-          }
-          issue(s_next);
-        }
-        if constexpr (decltype(with_math)::value)
-          compute_at(lo, (uint32_t)((it & (kRing - 1)) * T::SUB_BYTES), kv_begin + it * kSubTok,
-                     kv_end, scale_log2, lg);
-      }
-    };
-    if (__builtin_amdgcn_readfirstlane((int)active))
-      loop(std::true_type{});
-    else
-      loop(std::false_type{});
-    finish();
-  }
-
-  // LDS addresses (32-bit, ring slot 0) of the lane's operand reads: K rows
-  // k[tt][s] of read_k and V transpose reads v[tt][dt] of load_v.  With
-  // T::HALF_SAME the second 16-token half is a constant offset from the
-  // first and only [0][.] is kept.
-  struct LaneOff {
-    uint32_t k[T::HALF_SAME ? 1 : 2][KSTEPS];
-    uint32_t v[T::HALF_SAME ? 1 : 2][DTILES];
-  };
-  __device__ __forceinline__ LaneOff lane_offsets(const uint8_t* lds, int l16, int lg) const {
-    LaneOff lo;
-    const uint32_t base = (uint32_t)(uintptr_t)(AIOS_LDS const uint8_t*)lds;
-    constexpr int NH = T::HALF_SAME ? 1 : 2;
-#pragma unroll
-    for (int tt = 0; tt < NH; ++tt) {
-      const int t = tt * 16 + l16;
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s)
-        lo.k[tt][s] = base + (uint32_t)(t * T::ROWB + T::k_slot(t, s * 4 + lg) * 16);
-      const int tv = tt * 16 + lg * 4 + (l16 >> 2);
-#pragma unroll
-      for (int dt = 0; dt < DTILES; ++dt) {
-        const int dim = dt * 16 + 4 * (l16 & 3);
-        lo.v[tt][dt] = base + (uint32_t)(T::SUB_KB + tv * T::ROWB +
-                                         T::v_slot(tv, dim >> 3) * 16 + (dim & 7) * 2);
-      }
-    }
-    return lo;
-  }
-
-  // read_k / load_v on the ring slot at byte offset `sb` through the
-  // precomputed addresses: one add per address register and sub-tile, the
-  // second 16-token half (T::HALF_SAME) in the reads' offset field.
-  __device__ __forceinline__ void read_k_at(const LaneOff& lo, uint32_t sb,
-                                            bf16x8 (&kf)[2][KSTEPS]) {
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      const uint32_t a0 = lo.k[0][s] + sb;
-      const uint32_t a1 = T::HALF_SAME ? a0 + 16 * T::ROWB : lo.k[T::HALF_SAME ? 0 : 1][s] + sb;
-      kf[0][s] = *reinterpret_cast<AIOS_LDS const bf16x8*>((AIOS_LDS const uint8_t*)(uintptr_t)a0);
-      kf[1][s] = *reinterpret_cast<AIOS_LDS const bf16x8*>((AIOS_LDS const uint8_t*)(uintptr_t)a1);
-    }
-  }
-  __device__ __forceinline__ void load_v_at(const LaneOff& lo, uint32_t sb,
-                                            bf16x4 (&va)[DTILES][2]) {
-#pragma unroll
-    for (int dt = 0; dt < DTILES; ++dt) {
-      const uint32_t a0 = lo.v[0][dt] + sb;
-      va[dt][0] = lds_read_tr_at<0>(a0);
-      if constexpr (T::HALF_SAME)
-        va[dt][1] = lds_read_tr_at<16 * T::ROWB>(a0);
-      else
-        va[dt][1] = lds_read_tr_at<0>(lo.v[T::HALF_SAME ? 0 : 1][dt] + sb);
-    }
-  }
-  __device__ __forceinline__ void compute_at(const LaneOff& lo, uint32_t sb, int kv0, int kv_end,
-                                             float scale_log2, int lg) {
-    bf16x8 kf[2][KSTEPS];
-    bf16x4 va[DTILES][2];
-    f32x4 st[RT][2];
-    bf16x8 pb[RT];
-    read_k_at(lo, sb, kf);
-    load_v_at(lo, sb, va);
-    mma_s(kf, st);
-    softmax(st, kv0, kv_end, scale_log2, lg, pb);
-    accumulate(va, pb, kv_end - kv0, lg);
   }
 
   // Row totals (after the last compute).
@@ -569,6 +499,200 @@ struct TileEngine {
     mma_s(kf, st);
     softmax(st, kv0, kv_end, scale_log2, lg, pb);
     accumulate(va, pb, kv_end - kv0, lg);
+  }
+};
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// The tile engine with one 32-row tile per wavefront and
+// v_mfma_f32_32x32x16_bf16: the same math as TileEngine<D, CAUSAL, 2> (32
+// rows per wavefront, 128 per workgroup) with half the MFMA instructions
+// (each 32x32x16 does the work of two 16x16x32 and costs the SIMD about as
+// much vector issue as one), one row per lane pair, and a cheaper row max.
+//
+// Fragments (lane l, n = l % 32, h = l / 32), per 32-token sub-tile:
+//   S^T = K Q^T   A = K: token n, dims 16s + 8h .. +7 (one ds_read_b128 per
+//                 k-step s); B = Q^T: query row n, the same dims (kept in
+//                 registers); D: query row n, tokens 8j + 4h + i in
+//                 register 4j + i (j, i = 0..3)
+//   softmax       16 scores of row n in the lane, the other 16 in lane l ^ 32
+//   O^T += V^T P^T  per 32-dim tile and 16-token k-step, A = V^T from two LDS
+//                 transpose reads (lane l: dim n of tokens 4h .. 4h+3 and
+//                 8 + 4h .. 8 + 4h + 3, k-step 1 sixteen tokens on), B = P^T
+//                 = the lane's own scores 0..7 (k-step 0) and 8..15 (k-step 1)
+//                 as bf16 -- the permutation of the 16 tokens of a k-step is
+//                 the same on both sides, so no data moves between lanes.
+template <int D, bool CAUSAL>
+struct TileEngine32 {
+  using T = KVTile<D, true>;
+  static constexpr int KS = D / 16;  // k-steps of S^T
+  static constexpr int NT = D / 32;  // 32-dim tiles of O^T
+
+  bf16x8 qf[KS];
+  f32x16 o[NT];
+  f32x16 ol;       // row sums of P by MFMA (element 0 is read)
+  float m_run;     // the lane's row reference (log2 domain)
+  float nm;        // -(m_run, or 0 while m_run is -inf)
+  float l_run;     // row total, set by finish()
+  int limit;       // CAUSAL: last visible KV position of the lane's row
+  int min_limit;   // CAUSAL: smallest limit of any row of the workgroup
+
+  // Q fragments of the lane's row (B of S^T = K Q^T).
+  __device__ __forceinline__ void load_q(const bf16* q, bool ok) {
+    const int h = (threadIdx.x & 63) >> 5;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qf[s] = ok ? *reinterpret_cast<const bf16x8*>(q + s * 16 + h * 8) : bf16x8{};
+  }
+
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[t][i] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ol[i] = 0.f;
+    m_run = kNegInf;
+    nm = 0.f;
+    l_run = 0.f;
+  }
+
+  template <typename QLoad>
+  __device__ void run(uint8_t* lds, const uint8_t* kc, const uint8_t* vc, int64_t tok_bytes,
+                      int64_t num_pages, const int32_t* idx, int kv_begin, int kv_end,
+                      float scale_log2, QLoad&& qload, bool active = true) {
+    reset();
+    const LaneOff lo = lane_offsets(lds);
+    stream_kv<T>(lds, kc, vc, tok_bytes, num_pages, idx, kv_begin, kv_end, qload,
+                 [&](uint32_t sb, int kv0) { compute_at(lo, sb, kv0, kv_end, scale_log2); },
+                 active);
+    l_run = ol[0];
+  }
+
+  // LDS addresses (ring slot 0) of the lane's reads: K for each k-step; V
+  // for each 32-dim tile at its first token group (the other three groups,
+  // tokens +8, +16, +24, keep the slot: constant offsets).
+  struct LaneOff {
+    uint32_t k[KS];
+    uint32_t v[NT];
+  };
+  __device__ __forceinline__ LaneOff lane_offsets(const uint8_t* lds) const {
+    static_assert(D == 64 || D == 96 || D == 128, "head size");
+    LaneOff lo;
+    const int lane = threadIdx.x & 63;
+    const uint32_t base = (uint32_t)(uintptr_t)(AIOS_LDS const uint8_t*)lds;
+    const int t = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      lo.k[s] = base + (uint32_t)(t * T::ROWB + T::k_slot(t, 2 * s + h) * 16);
+    // transpose read: in each 16-lane group g, lane j supplies dims
+    // 4 (j % 4) .. +3 of token 4 (g / 2) + j / 4 within the tile's half g % 2
+    const int g = lane >> 4, j = lane & 15;
+    const int tv = 4 * (g >> 1) + (j >> 2);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int dim = nt * 32 + 16 * (g & 1) + 4 * (j & 3);
+      lo.v[nt] = base + (uint32_t)(T::SUB_KB + tv * T::ROWB + T::v_slot(tv, dim >> 3) * 16 +
+                                   (dim & 7) * 2);
+    }
+    return lo;
+  }
+
+  __device__ __forceinline__ void compute_at(const LaneOff& lo, uint32_t sb, int kv0, int kv_end,
+                                             float scale_log2) {
+    const int h = (threadIdx.x & 63) >> 5;
+    bf16x8 kf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      kf[s] = *reinterpret_cast<AIOS_LDS const bf16x8*>((AIOS_LDS const uint8_t*)(uintptr_t)(lo.k[s] + sb));
+    bf16x4 va[NT][4];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const uint32_t a = lo.v[nt] + sb;
+      va[nt][0] = lds_read_tr_at<0>(a);
+      va[nt][1] = lds_read_tr_at<8 * T::ROWB>(a);
+      va[nt][2] = lds_read_tr_at<16 * T::ROWB>(a);
+      va[nt][3] = lds_read_tr_at<24 * T::ROWB>(a);
+    }
+    f32x16 st;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) st[i] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) st = mfma32x32x16(kf[s], qf[s], st);
+
+    // Online softmax of the lane's row (the TileEngine rule: lazily moved
+    // reference, log2 domain).
+    const bool full = kv0 + kSubTok <= kv_end && (!CAUSAL || kv0 + kSubTok - 1 <= min_limit);
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = st[r];
+    if (__builtin_expect(!full, 0)) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int pos = kv0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        bool ok = pos < kv_end;
+        if (CAUSAL) ok = ok && pos <= limit;
+        if (!ok) x[r] = kNegInf;
+      }
+    }
+    float mx = vmax(vmax(vmax(vmax(x[0], x[1]), vmax(x[2], x[3])),
+                         vmax(vmax(x[4], x[5]), vmax(x[6], x[7]))),
+                    vmax(vmax(vmax(x[8], x[9]), vmax(x[10], x[11])),
+                         vmax(vmax(x[12], x[13]), vmax(x[14], x[15]))));
+    mx = xor32_max(mx) * scale_log2;
+    const bool need = mx > m_run + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float al = need ? fast_exp2(m_run - mx) : 1.f;
+      ol[0] *= al;  // the other elements of ol are never read
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[nt] *= al;
+      m_run = need ? mx : m_run;
+      nm = need ? -mx : nm;
+    }
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(x[r], scale_log2, nm));
+    const bf16x8 pb0 = __builtin_bit_cast(
+        bf16x8, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                           pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])));
+    const bf16x8 pb1 = __builtin_bit_cast(
+        bf16x8, make_uint4(pack_bf16x2(p[8], p[9]), pack_bf16x2(p[10], p[11]),
+                           pack_bf16x2(p[12], p[13]), pack_bf16x2(p[14], p[15])));
+
+    // V fragments complete; tokens >= n_valid zeroed (stale LDS must not
+    // meet P = 0 as a NaN).  va[nt][q] element e is token 8q + 4h + e.
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      lds_wait_tied(va[nt][0], va[nt][1]);
+      lds_wait_tied(va[nt][2], va[nt][3]);
+    }
+    const int n_valid = kv_end - kv0;
+    if (__builtin_expect(n_valid < kSubTok, 0)) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint64_t keep = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (8 * q + 4 * h + e < n_valid) keep |= 0xffffull << (16 * e);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          va[nt][q] = __builtin_bit_cast(bf16x4, __builtin_bit_cast(uint64_t, va[nt][q]) & keep);
+      }
+    }
+    const bf16x8 ones = (bf16x8)(bf16)1.0f;
+    ol = mfma32x32x16(ones, pb0, ol);
+    ol = mfma32x32x16(ones, pb1, ol);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const bf16x8 v0 = __builtin_shufflevector(va[nt][0], va[nt][1], 0, 1, 2, 3, 4, 5, 6, 7);
+      const bf16x8 v1 = __builtin_shufflevector(va[nt][2], va[nt][3], 0, 1, 2, 3, 4, 5, 6, 7);
+      o[nt] = mfma32x32x16(v0, pb0, o[nt]);
+      o[nt] = mfma32x32x16(v1, pb1, o[nt]);
+    }
   }
 };
 
