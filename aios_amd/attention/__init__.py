@@ -4,6 +4,7 @@ from .backend import (
     Mi355xAttentionBackend,
     Mi355xAttentionMetadata,
     Mi355xStaticDecodeMetadata,
+    Mi355xStaticPrefillMetadata,
     check_decode_preconditions,
 )
 
@@ -14,6 +15,7 @@ __all__ = [
     "Mi355xAttentionBackend",
     "Mi355xAttentionMetadata",
     "Mi355xStaticDecodeMetadata",
+    "Mi355xStaticPrefillMetadata",
     "SUPPORTED_HEAD_DIMS",
     "check_decode_preconditions",
 ]

@@ -101,6 +101,33 @@ class Mi355xStaticDecodeMetadata(Mi355xAttentionMetadata):
         )
 
 
+@dataclass
+class Mi355xStaticPrefillMetadata(Mi355xAttentionMetadata):
+    """Prefill metadata of one request (page-table row ``row_id``) on fixed
+    device buffers, for a prefill or LCP extension replayed from a HIP graph.
+
+    ``q_len`` new tokens; the plan is built for ``max_kv_len`` positions and
+    the kernel reads the request's actual KV length (cached + new) from
+    ``cu_seqlens_k_gpu``; ``refresh(kv_len)`` rewrites it and the flat page
+    indices on the device from a device scalar, with no host synchronisation.
+    """
+
+    row_ids_gpu: torch.Tensor | None = None
+    page_table: torch.Tensor | None = None
+    max_kv_len: int = 0
+    _ramp: torch.Tensor | None = None
+
+    def refresh(self, kv_len: torch.Tensor) -> None:
+        torch.mul(self._ramp, kv_len, out=self.cu_seqlens_k_gpu)
+        _lib.check(
+            _lib.lib().aios_build_indices(
+                self.page_table.data_ptr(), self.page_table.stride(0), self.row_ids_gpu.data_ptr(),
+                self.cu_seqlens_k_gpu.data_ptr(), 1, self.max_kv_len, self.indices.data_ptr(),
+                torch.cuda.current_stream(self.indices.device).cuda_stream),
+            "aios_build_indices",
+        )
+
+
 def check_decode_preconditions(indices: torch.Tensor, cu_seqlens_k: torch.Tensor,
                                out_loc: torch.Tensor | None, shared_prefix_len: int) -> None:
     """Raise ``ValueError`` unless the decode batch keeps the caller
@@ -313,6 +340,50 @@ class Mi355xAttentionBackend(BaseAttentionBackend):
             shared_prefix_len=shared_prefix_len,
             host_staging=cu_q,
             row_ids_gpu=row_ids.to(device=device, dtype=torch.int32).contiguous(),
+            page_table=page_table,
+            max_kv_len=max_kv_len,
+            _ramp=ramp,
+        )
+
+    def prepare_static_prefill(self, q_len: int, max_kv_len: int, page_table: torch.Tensor,
+                               row_id: int = 0) -> Mi355xStaticPrefillMetadata:
+        """Fixed-buffer prefill metadata for graph-replayed prefills of
+        ``q_len`` tokens against at most ``max_kv_len`` positions (see
+        :class:`Mi355xStaticPrefillMetadata`)."""
+        device = page_table.device
+        if page_table.dtype != torch.int32 or max_kv_len > page_table.shape[1]:
+            raise ValueError("max_kv_len exceeds the page-table row length")
+        if not 1 <= q_len <= max_kv_len:
+            raise ValueError("q_len must be within 1..max_kv_len")
+        cu_q = torch.tensor([0, q_len], dtype=torch.int32)
+        cu_k = torch.tensor([0, max_kv_len], dtype=torch.int32)
+        plan = _lib.AttnPlan()
+        _lib.check(
+            _lib.lib().aios_attn_plan(_lib.PHASE_PREFILL, cu_q.data_ptr(), cu_k.data_ptr(), 1,
+                                      self.num_heads, self.num_kv_heads, self.head_dim, 1, 0,
+                                      self.workspace_size, self.prefix_chunk_len,
+                                      self.suffix_split_len, plan),
+            "aios_attn_plan",
+        )
+        ramp = torch.arange(2, dtype=torch.int32, device=device)
+        return Mi355xStaticPrefillMetadata(
+            cu_seqlens_q_cpu=cu_q,
+            cu_seqlens_k_cpu=cu_k,
+            cu_seqlens_q_gpu=cu_q.to(device),
+            cu_seqlens_k_gpu=torch.zeros(2, dtype=torch.int32, device=device),
+            indices=torch.zeros(max_kv_len, dtype=torch.int32, device=device),
+            last_page_len_cpu=self._get_ones_cpu(1),
+            num_qo_heads=self.num_heads,
+            num_kv_heads=self.num_kv_heads,
+            head_dim=self.head_dim,
+            page_size=1,
+            pos_encoding_mode="NONE",
+            seq_lens_cpu=torch.tensor([max_kv_len], dtype=torch.int32),
+            dtype=torch.bfloat16,
+            plan=plan,
+            shared_prefix_len=0,
+            host_staging=cu_q,
+            row_ids_gpu=torch.tensor([row_id], dtype=torch.int32, device=device),
             page_table=page_table,
             max_kv_len=max_kv_len,
             _ramp=ramp,

@@ -283,11 +283,16 @@ class CandidateGroupEngine:
     # observed before each step is queued, so a superseded keystroke stops
     # within this many steps.
     RUN_AHEAD = 3
+    # Prefills and LCP extensions of at most this many new tokens are
+    # graph-replayed in graph mode (IME prompts and keystroke extensions; the
+    # few-row projection kernels take up to 64 rows).
+    MAX_GRAPHED_PREFILL = 64
 
     def __init__(self, rt: CandidateGroupRuntime, use_graphs: bool = True) -> None:
         self.rt = rt
         self.use_graphs = use_graphs
         self._graphs: OrderedDict[tuple, _DecodeGraph] = OrderedDict()
+        self._prefill_graphs: OrderedDict[tuple, _PrefillGraph] = OrderedDict()
         self._generation_id = 0
         self._active: CancellationToken | None = None
         self._gen_lock = threading.Lock()
@@ -454,7 +459,22 @@ class CandidateGroupEngine:
         return logits, prefix_pages, reused
 
     def _prefill(self, token_ids, cached_len: int, out_pages: torch.Tensor) -> torch.Tensor:
-        """Prefix prefill (cached_len 0) or LCP extension (ime.py:1170-1217)."""
+        """Prefix prefill (cached_len 0) or LCP extension (ime.py:1170-1217).
+        With graphs, prefills of up to MAX_GRAPHED_PREFILL new tokens replay a
+        graph captured per (new tokens, 64-aligned KV capacity)."""
+        q_len = len(token_ids) - cached_len
+        if self.use_graphs and 1 <= q_len <= self.MAX_GRAPHED_PREFILL:
+            kv_cap = min(-(-len(token_ids) // 64) * 64, self.rt.max_context)
+            key = (q_len, kv_cap)
+            g = self._prefill_graphs.get(key)
+            if g is None:
+                while len(self._prefill_graphs) >= self.MAX_GRAPHS:
+                    self._prefill_graphs.popitem(last=False)
+                g = _PrefillGraph(self, q_len, kv_cap)
+                self._prefill_graphs[key] = g
+            self._prefill_graphs.move_to_end(key)
+            # the graph's output buffer is overwritten by its next replay
+            return g.run(token_ids, cached_len, out_pages).clone()
         dev = self.rt.device
         req = Req(input_ids=torch.empty(len(token_ids), dtype=torch.long), cached_len=cached_len,
                   output_len=1, uid=0, sampling_params=SamplingParams(max_tokens=1), table_idx=0)
@@ -648,6 +668,65 @@ class CandidateGroupEngine:
             stop = "eos" if eos[i] else ("cancelled" if cancelled else "max_new_tokens")
             raw.append(Candidate(row, avg, stop))
         return raw, allocated, int(sum(cnt)), fed, cancelled
+
+
+class _PrefillGraph:
+    """Fixed buffers and the captured forward of one prefill shape: ``q_len``
+    new tokens of page-table row 0 against at most ``kv_cap`` positions
+    (cached + new).  One replay rebuilds the request's KV length and page
+    indices on the device, runs the model (the new tokens' K/V written to
+    their pages) and leaves the last token's logits in ``logits``."""
+
+    def __init__(self, eng: "CandidateGroupEngine", q_len: int, kv_cap: int) -> None:
+        rt = eng.rt
+        dev = rt.device
+        self.rt = rt
+        self.q_len = q_len
+        self.ids = torch.zeros(q_len, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(q_len, dtype=torch.int32, device=dev)
+        self.ramp = torch.arange(q_len, dtype=torch.int32, device=dev)
+        self.kv_len = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.out_loc = torch.zeros(q_len, dtype=torch.int32, device=dev)
+        self.md = rt.model.attn_backend.prepare_static_prefill(q_len, kv_cap, rt.page_table, 0)
+        req = Req(input_ids=torch.empty(q_len, dtype=torch.long), cached_len=0, output_len=1,
+                  uid=0, sampling_params=SamplingParams(max_tokens=1), table_idx=0)
+        self.batch = Batch(reqs=[req], phase="prefill")
+        self.batch.input_ids = self.ids
+        self.batch.positions = self.pos
+        self.batch.out_loc = self.out_loc
+        self.batch.attn_metadata = self.md
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.logits: torch.Tensor | None = None
+
+    def _body(self) -> torch.Tensor:
+        self.md.refresh(self.kv_len)
+        with self.rt.ctx.forward_batch(self.batch):
+            return self.rt.model.forward()
+
+    def run(self, token_ids, cached_len: int, out_pages: torch.Tensor) -> torch.Tensor:
+        if len(token_ids) - cached_len != self.q_len or out_pages.numel() != self.q_len:
+            raise ValueError("prefill graph used with another number of new tokens")
+        self.ids.copy_(torch.tensor(token_ids[cached_len:], dtype=torch.long))
+        torch.add(self.ramp, cached_len, out=self.pos)
+        self.kv_len.fill_(len(token_ids))
+        self.out_loc.copy_(out_pages)
+        if self.graph is not None:
+            self.graph.replay()
+            return self.logits
+        # First use: run eagerly on the capture stream (which also warms every
+        # library call there), then capture for the next ones.
+        dev = self.rt.device
+        cur = torch.cuda.current_stream(dev)
+        stream = torch.cuda.Stream(dev)
+        stream.wait_stream(cur)
+        with torch.cuda.stream(stream):
+            out = self._body()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            self.logits = self._body()
+        cur.wait_stream(stream)
+        self.graph = graph
+        return out
 
 
 class _DecodeGraph:

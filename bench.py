@@ -401,6 +401,15 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens=32,
         lat, gpu, pre, gen, rounds, attempts = [], [], [], 0, 0, 0
         replay_ms, replayed = 0.0, 0
         first = None
+        # A prefix-length range warms every length once first (graph mode
+        # captures one prefill graph per length): the timed runs measure the
+        # warm steady state, the reference's protocol.
+        lengths = [] if isinstance(prefix_tokens, int) else \
+            list(range(prefix_tokens[0], prefix_tokens[1] + 1))
+        for n_pre in lengths:
+            g = torch.Generator().manual_seed(seed + 500 + n_pre)
+            eng.reset_prefix_cache()
+            eng.complete(torch.randint(c.vocab_size, (n_pre + extend,), generator=g).tolist(), cfg)
         for i in range(warmups + runs):
             g = torch.Generator().manual_seed(seed + 1000 + i)
             n_pre = (prefix_tokens if isinstance(prefix_tokens, int) else

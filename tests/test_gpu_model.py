@@ -286,6 +286,47 @@ def test_graph_replay_matches_eager_minimind_0p1b():
     assert rt.cache_manager.available_size == rt.num_pages
 
 
+def test_graph_prefill_matches_eager():
+    """Graph-replayed prefills and LCP extensions (up to 64 new tokens) give
+    the eager prefill's logits and K/V rows bit for bit: on first use (the
+    capture), on replays with eager work in between, for extensions of a
+    cached prefix, and past the limit (eager in both engines).  The two
+    engines share one runtime (one global context); each case's prefix K/V
+    rows are copied out before the other engine runs it."""
+    c = MINIMIND_0P1B.with_layers(3)
+    w = init_weights(c, 12, "cpu")
+    rt = CandidateGroupRuntime(c, weights_to(w, "cuda"), "cuda", num_pages=512)
+    graphed = CandidateGroupEngine(rt, use_graphs=True)
+    eager = CandidateGroupEngine(rt, use_graphs=False)
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=2)
+    cases = [(5, 0), (9, 2), (9, 0), (31, 1), (5, 0), (40, 0), (70, 0), (9, 2)]
+    for trial, (n, ext) in enumerate(cases):
+        ids = _prefix(100 + trial, n + ext, c.vocab_size)
+        res, kv = [], []
+        for eng in (graphed, eager):
+            if ext:
+                eng.complete(ids[:n], cfg)
+            r = eng.complete(ids, cfg)
+            assert r.reused_prefix_tokens == (n if ext else 0)
+            pages = eng._prefix_pages.long()
+            kv.append((pages.clone(), [getattr(rt.kv_cache, kind)(layer)[pages].clone()
+                                       for layer in range(c.num_layers)
+                                       for kind in ("k_cache", "v_cache")]))
+            res.append(r)
+            eng.reset_prefix_cache()
+            torch.cuda.synchronize()
+        assert torch.equal(res[0].prefix_logits, res[1].prefix_logits), (n, ext)
+        assert [x.token_ids for x in res[0].raw_candidates] == \
+            [x.token_ids for x in res[1].raw_candidates]
+        # the allocator hands out different pages the second time; their rows agree
+        assert len(kv[0][0]) == len(kv[1][0]) == n + ext
+        assert all(torch.equal(a, b) for a, b in zip(kv[0][1], kv[1][1])), (n, ext)
+    assert sorted(graphed._prefill_graphs) == [(1, 64), (2, 64), (5, 64), (9, 64), (31, 64),
+                                               (40, 64)]
+    assert not eager._prefill_graphs
+    assert rt.cache_manager.available_size == rt.num_pages
+
+
 def test_graph_replay_cascade_prefix_and_neighbouring_lengths():
     """Long prefixes: the graph plans the cascade on a 64-aligned prefix and
     serves neighbouring prefix lengths from one capture."""
