@@ -1,6 +1,8 @@
 // Token selection with the raw log-probability of the chosen token:
-// greedy_kernel (argmax) and sample_kernel (stateless temperature / top-k /
-// top-p sampling, python/aios/engine/sample.py:12-160).
+// greedy_kernel (argmax), and stateless temperature / top-k / top-p sampling
+// (python/aios/engine/sample.py:12-160) by sample_resident_kernel (top-k
+// over rows of at most 16384 ids, the row held in registers) or
+// sample_kernel (longer rows, and every id in id order, streaming the row).
 //
 // Greedy:
 // One workgroup per row.  token = the first index of the row maximum of the
@@ -752,6 +754,570 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Row-resident sampling: top_k >= 1 (greedy included) over at most
+// kResMaxVocab ids.  One workgroup of NT threads per row (kResThreads); thread
+// t keeps the 8-id chunks q = c * NT + t (c < NC) of the row in registers, so
+// the row is read once and every later pass runs on registers:
+//  1. the forbidden ids set bits of an LDS bitmap (duplicates are harmless),
+//     read back as one byte per chunk;
+//  2. the raw maximum rmax (block max);
+//  3. one pass: the raw sum of exp, the sampling logits s (forbidden ids at
+//     -inf) and each id's code c = min((bits(rmax - s) >> 19) - (118 << 4)
+//     clamped at 0, 254): the float bits of a distance keep its order, so c
+//     grows with the distance below rmax (c >> 4: its binary octave from
+//     2^-9 to 2^7, c & 15: a sixteenth of that octave; 0 and 254 also take
+//     everything nearer and farther, -inf included; 255 marks the ids past
+//     the row).  A count of c >> 4 over 16 buckets (4-bit counters packed in
+//     one 64-bit register per chunk, at most 8 per counter), reduced with the
+//     sum of exp, finds the octave holding the k-th largest; when the ids up
+//     to that octave far outnumber k, a second count of c & 15 inside it
+//     narrows the bound to a sixteenth of an octave.  The ids with a code at
+//     or below the bound are an upper set of the sampling logits with at
+//     least k members, so they hold the top k;
+//  4. those candidates are written to LDS as composite keys (value key above
+//     ~id: distinct, larger = higher value, then lower id) at positions from
+//     per-slot ballots, and ordered: up to kResRankMax of them by rank
+//     counting (several threads per candidate, each over a contiguous run),
+//     more by a bitonic sort;
+//  5. more than kResCap candidates (ids tied at the bound): the k-th value
+//     key, and the id cut among its ties when those overflow too, are found
+//     by bisection with block counts, and exactly the top k are gathered;
+//  6. wavefront 0: softmax of value / temperature over the top k, the top-p
+//     cut and the inverse CDF with the formulas of sample_kernel (lane l owns
+//     entries [l * E, l * E + E), their exponentials kept in LDS; DPP lane
+//     sums and scans).
+// Measured on MI355X (24 rows, bf16, top_k 50): 12.3 us per launch at 16384
+// ids and 9.6 us at 6400, against 40-48 us for sample_kernel's three sweeps.
+constexpr int kResMaxVocab = 16384;  // ids per row at most
+constexpr int kResCap = 2048;     // candidates gathered and ordered at most
+constexpr int kResRankMax = 256;  // candidates ordered by rank counting at most
+static_assert(kResCap >= kSampleMaxTopK, "the exact top k fits the candidate buffer");
+
+template <typename T>
+struct ResKeyOf;
+template <>
+struct ResKeyOf<bf16> {
+  using Key = uint32_t;  // value key << 16 | (0xffff - id)
+  static constexpr int kIdBits = 16;
+};
+template <>
+struct ResKeyOf<float> {
+  using Key = unsigned long long;  // value key << 32 | (0xffffffff - id)
+  static constexpr int kIdBits = 32;
+};
+static_assert(kResMaxVocab <= (1 << 16), "ids fit the 16-bit field of the bf16 keys");
+
+template <typename Key, int NW>
+struct ResShared {
+  uint32_t fbits[kResMaxVocab / 32];   // forbidden ids, one bit each
+  alignas(16) uint32_t red[2][NW][8];  // per-wavefront packed counts
+  float fred[2][NW][2];                // per-wavefront max / sum
+  uint32_t ired[2][NW];                // per-wavefront counts (bisection)
+  uint32_t gscan[NW];                  // per-wavefront candidate counts
+  alignas(16) Key cand[kResCap];
+  Key top[kSampleMaxTopK];
+  float ev[kSampleMaxTopK];  // exp of the top k (wavefront 0)
+  int pos;
+};
+
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, false);
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+
+// Sums / maxima over the 64 lanes (every lane receives the result): DPP
+// inside each 16-lane row, then the gfx950 row and half swaps.
+__device__ __forceinline__ uint32_t lanes_sum_u(uint32_t x) {
+  x += dpp_u<0xB1>(x);
+  x += dpp_u<0x4E>(x);
+  x += dpp_u<0x141>(x);
+  x += dpp_u<0x140>(x);
+  auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = r[0] + r[1];
+  r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return r[0] + r[1];
+}
+__device__ __forceinline__ float lanes_max_f(float x) {
+  x = vmax(x, dpp_f<0xB1>(x));
+  x = vmax(x, dpp_f<0x4E>(x));
+  x = vmax(x, dpp_f<0x141>(x));
+  x = vmax(x, dpp_f<0x140>(x));
+  return xrow_max(x);
+}
+__device__ __forceinline__ float lanes_sum_f(float x) { return xrow_sum(row16_sum(x)); }
+
+// Inclusive prefix sums over the lanes: Hillis-Steele inside each 16-lane
+// row (row_shr 1, 2, 4, 8; lanes without a source add 0), then row 0's total
+// into row 1 and row 2's into row 3 (row_bcast:15), then the total of rows
+// 0-1 into rows 2-3 (row_bcast:31).
+__device__ __forceinline__ uint32_t lanes_scan_u(uint32_t x) {
+  x += dpp_u<0x111>(x);
+  x += dpp_u<0x112>(x);
+  x += dpp_u<0x114>(x);
+  x += dpp_u<0x118>(x);
+  x += dpp_u<0x142, 0xA>(x);
+  x += dpp_u<0x143, 0xC>(x);
+  return x;
+}
+__device__ __forceinline__ float lanes_scan_f(float x) {
+  x += dpp_f<0x111>(x);
+  x += dpp_f<0x112>(x);
+  x += dpp_f<0x114>(x);
+  x += dpp_f<0x118>(x);
+  x += dpp_f<0x142, 0xA>(x);
+  x += dpp_f<0x143, 0xC>(x);
+  return x;
+}
+
+// Eight consecutive logits of a row as fp32; ids at or past vocab read -inf
+// (a partial last chunk is read one id at a time).
+__device__ __forceinline__ void res_load8(const bf16* x, int i0, int vocab, float (&f)[8]) {
+  if (i0 + 8 <= vocab) {
+    const uint4 r = *reinterpret_cast<const uint4*>(x + i0);
+    f[0] = lo_bf16(r.x); f[1] = hi_bf16(r.x); f[2] = lo_bf16(r.y); f[3] = hi_bf16(r.y);
+    f[4] = lo_bf16(r.z); f[5] = hi_bf16(r.z); f[6] = lo_bf16(r.w); f[7] = hi_bf16(r.w);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      f[j] = i0 + j < vocab ? bf16_bits_to_float(__builtin_bit_cast(uint16_t, x[i0 + j])) : kNegInf;
+  }
+}
+__device__ __forceinline__ void res_load8(const float* x, int i0, int vocab, float (&f)[8]) {
+  if (i0 + 8 <= vocab) {
+    const float4 a = *reinterpret_cast<const float4*>(x + i0);
+    const float4 b = *reinterpret_cast<const float4*>(x + i0 + 4);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = i0 + j < vocab ? x[i0 + j] : kNegInf;
+  }
+}
+
+// Value key (LogitTraits::key) of an fp32 copy of a logit.
+__device__ __forceinline__ uint32_t res_vkey(float v, bf16*) {
+  return LogitTraits<bf16>::key(__float_as_uint(v) >> 16);
+}
+__device__ __forceinline__ uint32_t res_vkey(float v, float*) {
+  return LogitTraits<float>::key(__float_as_uint(v));
+}
+
+// Block totals of 16 counters held as 4-bit fields of one 64-bit register
+// per chunk (at most 8 per field): the fields are spread to bytes (at most
+// 8 * NC), then to 16-bit halves (bucket pairs (b, b + 4) per word), summed
+// over the lanes and across the wavefronts.  Every thread receives them.
+// A float partial (fsum, with its per-wavefront slots fred) is summed in the
+// same pass when fred is given; returns its block total.
+template <int NC, int NW>
+__device__ __forceinline__ float res_block_counts(const uint64_t (&acc)[NC], uint32_t (*red)[8],
+                                                  float (*fred)[2], float fsum, int lane, int wave,
+                                                  int (&tot)[16]) {
+  uint32_t bl[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const uint32_t lo = (uint32_t)acc[c], hi = (uint32_t)(acc[c] >> 32);
+    bl[0] += lo & 0x0f0f0f0fu;         // byte b: bucket 2b
+    bl[1] += (lo >> 4) & 0x0f0f0f0fu;  // bucket 2b + 1
+    bl[2] += hi & 0x0f0f0f0fu;         // bucket 8 + 2b
+    bl[3] += (hi >> 4) & 0x0f0f0f0fu;  // bucket 9 + 2b
+  }
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[2 * i] = bl[i] & 0x00ff00ffu;             // bytes 0, 2
+    w[2 * i + 1] = (bl[i] >> 8) & 0x00ff00ffu;  // bytes 1, 3
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w[i] = lanes_sum_u(w[i]);
+  if (fred != nullptr) fsum = lanes_sum_f(fsum);
+  if (lane == 0) {
+    reinterpret_cast<uint4*>(red[wave])[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    reinterpret_cast<uint4*>(red[wave])[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    if (fred != nullptr) fred[wave][0] = fsum;
+  }
+  __syncthreads();
+  float ftot = 0.f;
+  if (fred != nullptr)
+#pragma unroll
+    for (int v = 0; v < NW; ++v) ftot += fred[v][0];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w[i] = 0u;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    const uint4 p = reinterpret_cast<const uint4*>(red[v])[0];
+    const uint4 q = reinterpret_cast<const uint4*>(red[v])[1];
+    w[0] += p.x; w[1] += p.y; w[2] += p.z; w[3] += p.w;
+    w[4] += q.x; w[5] += q.y; w[6] += q.z; w[7] += q.w;
+  }
+  // w[2i + h] holds bytes h and h + 2 of bl[i]: bl[0] byte b = bucket 2b,
+  // bl[1] byte b = 2b + 1, bl[2] byte b = 8 + 2b, bl[3] byte b = 9 + 2b.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int base = (i & 1) + (i >> 1) * 8;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      tot[base + 2 * h] = (int)(w[2 * i + h] & 0xffffu);
+      tot[base + 2 * h + 4] = (int)(w[2 * i + h] >> 16);
+    }
+  }
+  return ftot;
+}
+
+template <typename T, int NT, int NC>
+__global__ __launch_bounds__(NT) void sample_resident_kernel(SampleArgs a) {
+  constexpr int NW = NT / 64;
+  static_assert(NT * 8 * NC <= kResMaxVocab && kSampleMaxForbidden <= NT, "row and lists fit");
+  static_assert(NC * 8 <= 32, "a thread's ids index 32-bit masks");
+  using L = LogitTraits<T>;
+  using Key = typename ResKeyOf<T>::Key;
+  constexpr int kIdBits = ResKeyOf<T>::kIdBits;
+  constexpr Key kIdMask = (Key)((1ull << kIdBits) - 1);
+  __shared__ ResShared<Key, NW> sh;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int row = blockIdx.x;
+  const int vocab = a.vocab;
+  const T* x = static_cast<const T*>(a.logits) + (int64_t)row * a.row_stride;
+  const uint32_t neg_key = L::key(L::kBits == 16 ? 0xff80u : 0xff800000u);
+
+  // The row (chunk c of this thread: ids 8 (c * NT + tid) + j).
+  float v[NC][8];
+  uint32_t valid = 0;  // bit 8c + j: id inside the row
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int i0 = (c * NT + tid) * 8;
+    res_load8(x, i0, vocab, v[c]);
+    const int nv = min(max(vocab - i0, 0), 8);
+    valid |= ((1u << nv) - 1u) << (8 * c);
+  }
+  const int64_t step = a.step != nullptr ? *a.step : 0;
+  // this thread's forbidden id (if any): the global list while
+  // step < forbid_before_step, then row r's list
+  int fid = -1;
+  if (tid < a.n_forbidden) {
+    const int32_t f = a.forbidden[tid];
+    fid = (step < a.forbid_before_step && f >= 0 && f < vocab) ? f : -1;
+  } else if (tid < a.n_forbidden + a.row_forbidden_count) {
+    const int64_t f = a.forbidden_by_row[(int64_t)row * a.row_forbidden_count + tid - a.n_forbidden];
+    fid = (f >= 0 && f < vocab) ? (int)f : -1;
+  }
+  const int64_t col = step < 0 ? 0 : (step >= a.uniform_count ? a.uniform_count - 1 : step);
+  const float u = a.uniforms != nullptr ? a.uniforms[(int64_t)row * a.uniform_stride + col] : 0.5f;
+
+  // 1. forbidden bitmap
+  for (int i = tid; i < (vocab + 31) / 32; i += NT) sh.fbits[i] = 0u;
+  __syncthreads();
+  if (fid >= 0) atomicOr(&sh.fbits[fid >> 5], 1u << (fid & 31));
+
+  // 2. raw maximum (its barrier also publishes the bitmap)
+  float rm = kNegInf;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) rm = vmax(rm, v[c][j]);
+  rm = lanes_max_f(rm);
+  if (lane == 0) sh.fred[0][wave][0] = rm;
+  __syncthreads();
+  float rmax = kNegInf;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) rmax = vmax(rmax, sh.fred[0][w][0]);
+
+  // raw sum of exp; sampling logits (forbidden ids at -inf); each id's code
+  // (the distance to rmax: an upper bound of the sampling logits, so codes
+  // still grow as sampling logits fall) and the octave count.  Ids past the
+  // row read -inf (code 255) and are taken out of bucket 15 afterwards.
+  const float mu = rmax == kNegInf ? 0.f : rmax * kLog2e;
+  float rs = 0.f;
+  uint32_t code[NC][2];  // four 8-bit codes per word
+  uint64_t acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int q = c * NT + tid;
+    const uint32_t fb = q * 8 < vocab ? reinterpret_cast<const uint8_t*>(sh.fbits)[q] : 0u;
+    code[c][0] = code[c][1] = 0u;
+    acc[c] = 0ull;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      rs += fast_exp2(v[c][j] * kLog2e - mu);
+      if ((fb >> j) & 1u) v[c][j] = kNegInf;
+      const float d = rmax - v[c][j];  // +0 at the maximum; inf or NaN at -inf
+      const uint32_t eb = __float_as_uint(d) >> 19;
+      const uint32_t cb = min(eb - min(eb, 118u << 4), 254u);
+      code[c][j >> 2] |= cb << (8 * (j & 3));
+      acc[c] += 1ull << ((cb >> 4) * 4);
+    }
+    // ids past the row: code 255 (counted in bucket 15, taken out below)
+    const int nv = min(max(vocab - q * 8, 0), 8);
+    if (nv < 8) {
+      code[c][0] |= nv >= 4 ? 0u : 0xffffffffu << (8 * nv);
+      code[c][1] |= nv <= 4 ? 0xffffffffu : 0xffffffffu << (8 * (nv - 4));
+    }
+  }
+  int tot[16];
+  const float rsum = res_block_counts<NC, NW>(acc, sh.red[0], sh.fred[1], rs, lane, wave, tot);
+  const int n_pad_ids = NC * NT * 8 - vocab;  // ids past the row, all in bucket 15
+  tot[15] -= n_pad_ids;
+  const float log_z = rmax + logf(rsum);
+  const int k = min(a.top_k, vocab);
+  int oct = 15, below = 0;
+  {
+    int cum = 0;
+    bool found = false;
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      if (!found && cum + tot[b] >= k) {
+        found = true;
+        oct = b;
+        below = cum;
+      }
+      cum += tot[b];
+    }
+  }
+  // (code 255 marks ids past the row: the bound stays below it)
+  int bound = min(oct * 16 + 15, 254);
+  int n = below + tot[oct];
+  // the sixteenths of that octave when it holds many more than k
+  if (n > 192 && n > k + (k >> 2)) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      acc[c] = 0ull;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t cb = (code[c][j >> 2] >> (8 * (j & 3))) & 0xffu;
+        acc[c] += (uint64_t)((cb >> 4) == (uint32_t)oct ? 1u : 0u) << ((cb & 15u) * 4);
+      }
+    }
+    res_block_counts<NC, NW>(acc, sh.red[1], nullptr, 0.f, lane, wave, tot);
+    if (oct == 15) tot[15] -= n_pad_ids;
+    int cum = below;
+    bool found = false;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      if (!found && cum + tot[s] >= k) {
+        found = true;
+        bound = oct * 16 + s;
+        n = cum + tot[s];
+      }
+      cum += tot[s];
+    }
+  }
+
+  auto id_of = [&](int c, int j) { return (c * NT + tid) * 8 + j; };
+  auto ckey = [&](int c, int j) {
+    return ((Key)res_vkey(v[c][j], (T*)nullptr) << kIdBits) | (kIdMask - (Key)id_of(c, j));
+  };
+  // Writes the ids for which pred(c, j) holds to sh.cand (wavefront by
+  // wavefront, id slot by id slot: one ballot per slot, positions from the
+  // wavefront totals and mbcnt) and zero keys after them up to the next
+  // power of two; returns how many.
+  auto gather = [&](auto&& pred) -> int {
+    uint32_t wcnt = 0u;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wcnt += __popcll(__ballot(pred(c, j)));
+    if (lane == 0) sh.gscan[wave] = wcnt;
+    __syncthreads();
+    uint32_t pos = 0u, total = 0u;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t t = sh.gscan[w];
+      pos += w < wave ? t : 0u;
+      total += t;
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool pr = pred(c, j);
+        const uint64_t mk = __ballot(pr);
+        if (mk != 0ull) {
+          const uint32_t at = pos + __builtin_amdgcn_mbcnt_hi(
+                                        (uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+          if (pr && at < (uint32_t)kResCap) sh.cand[at] = ckey(c, j);
+          pos += __popcll(mk);
+        }
+      }
+    const int cnt = (int)min(total, (uint32_t)kResCap);
+    int npad = 1;
+    while (npad < cnt) npad <<= 1;
+    for (int i = cnt + tid; i < npad; i += NT) sh.cand[i] = 0;
+    __syncthreads();
+    return cnt;
+  };
+
+  auto in_row = [&](int c, int j) { return ((valid >> (8 * c + j)) & 1u) != 0u; };
+  if (n <= kResCap) {
+    n = gather([&](int c, int j) {
+      return (int)((code[c][j >> 2] >> (8 * (j & 3))) & 0xffu) <= bound;
+    });
+  } else {
+    // 5. ties at the bound overflow the buffer: bisection with block counts
+    int parity = 0;
+    auto count = [&](auto&& pred) -> int {
+      uint32_t cnt = 0u;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          cnt += (((valid >> (8 * c + j)) & 1u) && pred(c, j)) ? 1u : 0u;
+      cnt = lanes_sum_u(cnt);
+      if (lane == 0) sh.ired[parity][wave] = cnt;
+      __syncthreads();
+      uint32_t t = 0u;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) t += sh.ired[parity][w];
+      parity ^= 1;
+      return (int)t;
+    };
+    // the k-th largest value key: the largest t with count(key >= t) >= k
+    uint32_t lo = 0u, hi = L::kBits == 16 ? 0xffffu : 0xffffffffu;
+    int n_ge = vocab;
+    while (lo < hi) {
+      const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
+      const int cm = count([&](int c, int j) { return res_vkey(v[c][j], (T*)nullptr) >= mid; });
+      if (cm >= k) {
+        lo = mid;
+        n_ge = cm;
+      } else {
+        hi = mid - 1;
+      }
+    }
+    const uint32_t tkey = lo;
+    if (n_ge <= kResCap) {
+      n = gather([&](int c, int j) { return in_row(c, j) && res_vkey(v[c][j], (T*)nullptr) >= tkey; });
+    } else {
+      // the lowest ids of the ties: the smallest m with
+      // count(key == tkey, id <= m) >= k - count(key > tkey)
+      const int need = k - count([&](int c, int j) { return res_vkey(v[c][j], (T*)nullptr) > tkey; });
+      int ilo = 0, ihi = vocab - 1;
+      while (ilo < ihi) {
+        const int mid = (ilo + ihi) >> 1;
+        const int cm = count([&](int c, int j) {
+          return res_vkey(v[c][j], (T*)nullptr) == tkey && id_of(c, j) <= mid;
+        });
+        if (cm >= need) ihi = mid;
+        else ilo = mid + 1;
+      }
+      n = gather([&](int c, int j) {
+        const uint32_t kk = res_vkey(v[c][j], (T*)nullptr);
+        return in_row(c, j) && (kk > tkey || (kk == tkey && id_of(c, j) <= ilo));
+      });
+    }
+  }
+
+  // 4. order the candidates; the first k go to sh.top
+  // (the gather left zero keys, below every real key, up to npad)
+  int npad = 1;
+  while (npad < n) npad <<= 1;
+  if (n <= kResRankMax) {
+    // tpe threads per candidate, each counting the larger keys in its own
+    // contiguous run of L entries
+    const int tpe = min(min(64, NT / npad), npad);
+    const int L = npad / tpe;
+    const int e = tid / tpe;
+    const int p = tid - e * tpe;
+    int r = 0;
+    Key ce = 0;
+    if (e < n) {
+      ce = sh.cand[e];
+      const Key* run = sh.cand + p * L;
+      constexpr int KV = 16 / sizeof(Key);  // keys per 16-byte read
+      if (L % KV == 0) {
+        for (int j = 0; j < L; j += KV) {
+          const uint4 q = *reinterpret_cast<const uint4*>(run + j);
+          if constexpr (KV == 4) {
+            r += (q.x > ce ? 1 : 0) + (q.y > ce ? 1 : 0) + (q.z > ce ? 1 : 0) + (q.w > ce ? 1 : 0);
+          } else {
+            r += ((((Key)q.y << 32) | q.x) > ce ? 1 : 0) + ((((Key)q.w << 32) | q.z) > ce ? 1 : 0);
+          }
+        }
+      } else {
+        for (int j = 0; j < L; ++j) r += run[j] > ce ? 1 : 0;
+      }
+    }
+    for (int off = 1; off < tpe; off <<= 1) r += __shfl_xor(r, off);
+    if (e < n && p == 0 && r < k) sh.top[r] = ce;
+    __syncthreads();
+  } else {
+    for (int size = 2; size <= npad; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < (npad >> 1); i += NT) {
+          const int pos = 2 * i - (i & (stride - 1));
+          const int oth = pos + stride;
+          const bool desc = (pos & size) == 0;
+          const Key p0 = sh.cand[pos], p1 = sh.cand[oth];
+          if (desc ? (p0 < p1) : (p0 > p1)) {
+            sh.cand[pos] = p1;
+            sh.cand[oth] = p0;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int i = tid; i < k; i += NT) sh.top[i] = sh.cand[i];
+    __syncthreads();
+  }
+
+  // 6. softmax, top-p cut, inverse CDF (wavefront 0; lane l owns entries
+  // [l * E, l * E + E))
+  auto value_of = [&](Key ck) { return L::value((uint32_t)(ck >> kIdBits)); };
+  if (wave == 0 && !a.greedy) {
+    const int E = (k + 63) / 64;
+    const int i0 = lane * E;
+    const int i1 = min(i0 + E, k);
+    const float m = value_of(sh.top[0]) / a.temperature;
+    float loc = 0.f;
+    for (int i = i0; i < i1; ++i) {
+      const float ei = expf(value_of(sh.top[i]) / a.temperature - m);
+      sh.ev[i] = ei;
+      loc += ei;
+    }
+    const float sum = lanes_sum_f(loc);
+    float sum2 = sum;
+    if (a.top_p < 1.f) {
+      // cumulative probability before each entry; remove where it exceeds top_p
+      float pl = 0.f;
+      for (int i = i0; i < i1; ++i) pl += sh.ev[i] / sum;
+      float c = lanes_scan_f(pl) - pl;
+      float loc2 = 0.f;
+      for (int i = i0; i < i1; ++i) {
+        const float ei = sh.ev[i];
+        const bool remove = i > 0 && c > a.top_p;
+        c += ei / sum;
+        if (remove) sh.ev[i] = 0.f;
+        else loc2 += ei;
+      }
+      sum2 = lanes_sum_f(loc2);
+    }
+    float pl = 0.f;
+    for (int i = i0; i < i1; ++i) pl += sh.ev[i] / sum2;
+    float c = lanes_scan_f(pl) - pl;
+    uint32_t nb = 0u;
+    for (int i = i0; i < i1; ++i) {
+      c += sh.ev[i] / sum2;
+      nb += c < u ? 1u : 0u;
+    }
+    nb = lanes_sum_u(nb);
+    if (lane == 0) sh.pos = min((int)nb, k - 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const Key ck = sh.top[a.greedy ? 0 : sh.pos];
+    const int chosen = (int)(kIdMask - (ck & kIdMask));
+    const uint32_t vk = (uint32_t)(ck >> kIdBits);
+    // a forbidden (or -inf) id carries the -inf key: its raw logit is read
+    const float raw = vk == neg_key ? L::to_float(L::load1(x + chosen)) : L::value(vk);
+    a.token_out[row] = chosen;
+    a.logprob_out[row] = raw - log_z;
+  }
+}
+
 // One uniform per (row, step): SplitMix64 of seed + (step + 1) * golden
 // ratio, 53 high bits + 0.5 over 2^53, rounded to fp32 (sample.py:12-47).
 __global__ void uniforms_kernel(const int64_t* __restrict__ seeds, int32_t rows, int32_t steps,
@@ -768,8 +1334,32 @@ __global__ void uniforms_kernel(const int64_t* __restrict__ seeds, int32_t rows,
 
 }  // namespace
 
+constexpr int kResThreads = 512;  // threads per row of the row-resident kernel
+
+template <typename T>
+static void launch_resident(const SampleArgs& a, hipStream_t stream) {
+  constexpr int NT = kResThreads;
+  const dim3 grid(a.rows), block(NT);
+  if (a.vocab <= NT * 8)
+    sample_resident_kernel<T, NT, 1><<<grid, block, 0, stream>>>(a);
+  else if (a.vocab <= NT * 16)
+    sample_resident_kernel<T, NT, 2><<<grid, block, 0, stream>>>(a);
+  else
+    sample_resident_kernel<T, NT, kResMaxVocab / (NT * 8)><<<grid, block, 0, stream>>>(a);
+}
+
 hipError_t sample_rows(const SampleArgs& a, hipStream_t stream) {
   if (a.rows == 0) return hipSuccess;
+  // top-k (greedy included) over a row that fits the registers of one
+  // workgroup: the row-resident kernel; every id in id order (top_k 0) and
+  // longer rows: the streaming kernel
+  if (a.top_k >= 1 && a.vocab <= kResMaxVocab) {
+    if (a.elem_bytes == 2)
+      launch_resident<bf16>(a, stream);
+    else
+      launch_resident<float>(a, stream);
+    return hipGetLastError();
+  }
   if (a.elem_bytes == 2)
     sample_kernel<bf16><<<dim3(a.rows), dim3(kSampleThreads), 0, stream>>>(a);
   else

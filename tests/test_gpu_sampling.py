@@ -110,7 +110,7 @@ PARAMS = [
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("vocab", [6400, 151936, 37])
+@pytest.mark.parametrize("vocab", [6400, 151936, 37, 4100, 16384])
 @pytest.mark.parametrize("pi", range(len(PARAMS)))
 def test_sample_matches_oracle(dtype, vocab, pi):
     params = PARAMS[pi]
@@ -143,6 +143,41 @@ def test_sample_ties_and_forbidden():
     tok, _ = Sampler(SamplingParams()).sample_with_logprobs(x[:2], forbidden_token_ids=(17, 4000))
     want = [int(((x[r].float() == 1.5).nonzero()[0]).item()) for r in range(2)]
     assert tok[:, 0].tolist() == want
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_sample_ties_beyond_the_candidate_buffer(dtype):
+    """Four distinct values over 16384 ids: about 4096 ids tie at each value,
+    so the ids at or above the k-th value overflow the row-resident kernel's
+    2048-entry candidate buffer and the exact k-th value key and id cut are
+    found by bisection; the lowest tied ids must be taken.  Forbidden ids
+    among the top ties shift the cut."""
+    rows, vocab = 8, 16384
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x = (torch.randint(0, 4, (rows, vocab), generator=g, device="cuda").to(torch.float32) * 0.5).to(dtype)
+    u = stateless_uniforms([500 + r for r in range(rows)], 1, torch.device("cuda"))[:, 0]
+    top = [int((x[r].float() == 1.5).nonzero()[0].item()) for r in range(rows)]
+    by_row = torch.tensor([[t, t + 1] for t in top], dtype=torch.int64, device="cuda")
+    for params in (SamplingParams(temperature=0.5, top_k=50, top_p=0.9),
+                   SamplingParams(temperature=1.0, top_k=1024, top_p=1.0),
+                   SamplingParams(temperature=0.0)):
+        _check_rows(x, params, u)
+        _check_rows(x, params, u, forbidden=(3,), by_row=by_row)
+
+
+def test_sample_all_equal_row_takes_the_lowest_ids():
+    """Every id ties: greedy takes id 0 (or the first one not forbidden) and
+    top-k sampling draws among ids 0..k-1."""
+    rows, vocab = 4, 16384
+    x = torch.zeros(rows, vocab, dtype=torch.bfloat16, device="cuda")
+    tok, _ = Sampler(SamplingParams()).sample_with_logprobs(x)
+    assert tok[:, 0].tolist() == [0] * rows
+    tok, _ = Sampler(SamplingParams()).sample_with_logprobs(x, forbidden_token_ids=(0, 1))
+    assert tok[:, 0].tolist() == [2] * rows
+    u = torch.tensor([0.0, 0.3, 0.7, 0.999], device="cuda")
+    tok, lp = Sampler(SamplingParams(temperature=1.0, top_k=8)).sample_with_logprobs(x, uniforms=u)
+    assert tok[:, 0].tolist() == [0, 2, 5, 7]
+    assert torch.allclose(lp[:, 0].cpu(), torch.full((rows,), -float(np.log(vocab))), atol=1e-5)
 
 
 def test_sample_step_reads_device_step_and_forbid_window():
