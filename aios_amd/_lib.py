@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "aios_attn_prefill",
     "aios_attn_decode",
     "aios_attn_append_decode",
+    "aios_attn_append_decode_rope",
     "aios_attn_decode_noalloc",
     "aios_build_indices",
     "aios_rmsnorm",
@@ -130,6 +131,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.aios_attn_append_decode.argtypes = [
         ctypes.POINTER(AttnPlan), _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp,
         _vp, _vp, _i64, _f32, _vp,
+    ]
+    lib.aios_attn_append_decode_rope.restype = ctypes.c_int
+    lib.aios_attn_append_decode_rope.argtypes = [
+        ctypes.POINTER(AttnPlan), _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp,
+        _vp, _vp, _vp, _vp, _i64, _vp, _f32, _vp, _vp, _i64, _f32, _vp,
     ]
     lib.aios_build_indices.restype = ctypes.c_int
     lib.aios_build_indices.argtypes = [_vp, _i64, _vp, _vp, _i32, _i32, _vp, _vp]

@@ -402,6 +402,65 @@ class Mi355xAttentionBackend(BaseAttentionBackend):
             return self._prefill(q, k, v, paged_kv_cache, layer_id, batch)
         return self._decode(q, k, v, paged_kv_cache, layer_id, batch)
 
+    # Head sizes whose decoder layers take the q/k norm + rotation inside the
+    # decode launch.  Measured on MI355X (graph-replayed CandidateGroup step,
+    # the two forms back to back): 64 (MiniMind-IME 0.1B) 441 -> 430 us;
+    # 96 (MiniMind 0.1B) 445 -> 445 us; 128 (Qwen3-0.6B) 1304 -> 1339 us, its
+    # rotation inputs pushing the decode kernel past the register file.
+    ROPE_IN_DECODE_HEAD_DIMS = (64,)
+
+    def decode_rope_applies(self, batch: Batch) -> bool:
+        """Whether forward_rope takes this batch: an appending decode batch
+        (Batch.fused_append) whose new tokens lie after the shared prefix,
+        at a head size listed in ROPE_IN_DECODE_HEAD_DIMS."""
+        if self.head_dim not in self.ROPE_IN_DECODE_HEAD_DIMS:
+            return False
+        if not batch.is_decode or not batch.fused_append:
+            return False
+        md = batch.attn_metadata
+        return (isinstance(md, Mi355xAttentionMetadata)
+                and md.plan.prefix_len < md.plan.min_kv_len
+                and batch.out_loc.dtype == torch.int32)
+
+    def forward_rope(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     q_norm: torch.Tensor, k_norm: torch.Tensor, cos: torch.Tensor,
+                     sin: torch.Tensor, positions: torch.Tensor, eps: float,
+                     paged_kv_cache: MHAKVCache, layer_id: int, batch: Batch) -> torch.Tensor:
+        """The q/k RMSNorm + rotary embedding of Qwen3Attention.forward
+        (python/aios/models/qwen3.py:52-67), store_kv and the decode run
+        (python/aios/attention/flashinfer.py:374-394) in one launch, for a
+        batch decode_rope_applies accepts; q and k are the raw projections,
+        cos / sin the rotary tables rounded to bf16."""
+        if not (batch.is_decode and batch.fused_append
+                and isinstance(batch.attn_metadata, Mi355xAttentionMetadata)
+                and batch.attn_metadata.plan.prefix_len < batch.attn_metadata.plan.min_kv_len
+                and batch.out_loc.dtype == torch.int32):
+            raise ValueError("forward_rope needs an appending decode batch (Batch.fused_append) "
+                             "whose new tokens lie after the shared prefix")
+        bsz = batch.size
+        metadata = batch.attn_metadata
+        self._check_q(q)
+        if q.size(0) != bsz:
+            raise ValueError("decode batch must contain one flat token per request")
+        if k.shape != v.shape or k.shape[1:] != (self.num_kv_heads, self.head_dim):
+            raise ValueError("K/V input shape does not match the cache layout")
+        plan = metadata.plan
+        out_loc = batch.out_loc.view(-1)
+        if out_loc.numel() != k.shape[0]:
+            raise ValueError("KV write indices and K/V tensors must have matching token counts")
+        if self.validate and layer_id == 0 and not torch.cuda.is_current_stream_capturing():
+            check_decode_preconditions(metadata.indices, metadata.cu_seqlens_k_gpu, out_loc,
+                                       metadata.shared_prefix_len)
+        ws = self._get_workspace(q.device) if plan.ws_bytes else None
+        k_cache, v_cache = self._layer_caches(paged_kv_cache, layer_id)
+        out = paged.append_decode_rope(plan, q, k, v, out_loc.contiguous(),
+                                       k_cache.view(-1, self.num_kv_heads, self.head_dim),
+                                       v_cache.view(-1, self.num_kv_heads, self.head_dim),
+                                       metadata.indices, metadata.cu_seqlens_k_gpu, q_norm, k_norm,
+                                       cos, sin, positions, eps, workspace=ws,
+                                       sm_scale=self.sm_scale)
+        return out.reshape(bsz, -1)
+
     def _check_q(self, q: torch.Tensor) -> None:
         if q.ndim != 3 or q.shape[1] != self.num_heads or q.shape[2] != self.head_dim:
             raise ValueError("q must have shape (tokens, num_qo_heads, head_dim)")

@@ -284,10 +284,22 @@ struct NewKV {
   const int32_t* out_loc;
 };
 
+// Per-head q / k RMSNorm + RoPE applied on load (aios_attn_append_decode_rope).
+struct QkRopeIn {
+  const void* q_norm;
+  const void* k_norm;
+  const void* cos;
+  const void* sin;
+  int64_t rows;
+  const int32_t* positions;
+  float eps;
+};
+
 int decode_impl(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
                 const void* k_cache, const void* v_cache, int64_t kv_num_pages,
                 const int32_t* indices, const int32_t* cu_k, void* out, void* workspace,
-                int64_t workspace_bytes, float sm_scale, void* stream, const NewKV* nk) {
+                int64_t workspace_bytes, float sm_scale, void* stream, const NewKV* nk,
+                const QkRopeIn* ro = nullptr) {
   int rc = check_plan(p, AIOS_PHASE_DECODE);
   if (rc) return rc;
   if (p->batch_size == 0) return AIOS_OK;
@@ -360,6 +372,23 @@ int decode_impl(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
     a.v_new_stride = nk->v_stride;
     a.out_loc = nk->out_loc;
   }
+  if (ro) {
+    if (!nk) return fail(AIOS_ERR_INVALID, "append_decode_rope: the rotation needs the new K rows");
+    if (!ro->q_norm || !ro->k_norm || !ro->cos || !ro->sin || !ro->positions)
+      return fail(AIOS_ERR_INVALID, "append_decode_rope: null pointer");
+    if (ro->rows < 1) return fail(AIOS_ERR_INVALID, "append_decode_rope: empty rotation table");
+    if ((((uintptr_t)ro->q_norm | (uintptr_t)ro->k_norm | (uintptr_t)ro->cos |
+          (uintptr_t)ro->sin | (uintptr_t)nk->k) & 15) != 0)
+      return fail(AIOS_ERR_INVALID,
+                  "append_decode_rope: norm weights, tables and K rows must be 16-byte aligned");
+    a.q_norm = static_cast<const aios::bf16*>(ro->q_norm);
+    a.k_norm = static_cast<const aios::bf16*>(ro->k_norm);
+    a.rope_cos = static_cast<const aios::bf16*>(ro->cos);
+    a.rope_sin = static_cast<const aios::bf16*>(ro->sin);
+    a.rope_rows = ro->rows;
+    a.positions = ro->positions;
+    a.norm_eps = ro->eps;
+  }
   if (mask & 1) {
     rc = check_hip(aios::launch_decode_main(D, a, s), "decode launch");
     if (rc) return rc;
@@ -390,6 +419,21 @@ int aios_attn_append_decode(const aios_attn_plan_t* p, const void* q, int64_t q_
   const NewKV nk = {k_new, k_tok_stride, v_new, v_tok_stride, out_loc};
   return decode_impl(p, q, q_tok_stride, k_cache, v_cache, kv_num_pages, indices, cu_k, out,
                      workspace, workspace_bytes, sm_scale, stream, &nk);
+}
+
+int aios_attn_append_decode_rope(const aios_attn_plan_t* p, const void* q, int64_t q_tok_stride,
+                                 const void* k_new, int64_t k_tok_stride, const void* v_new,
+                                 int64_t v_tok_stride, const int32_t* out_loc, void* k_cache,
+                                 void* v_cache, int64_t kv_num_pages, const int32_t* indices,
+                                 const int32_t* cu_k, const void* q_norm, const void* k_norm,
+                                 const void* rope_cos, const void* rope_sin, int64_t rope_rows,
+                                 const int32_t* positions, float norm_eps, void* out,
+                                 void* workspace, int64_t workspace_bytes, float sm_scale,
+                                 void* stream) {
+  const NewKV nk = {k_new, k_tok_stride, v_new, v_tok_stride, out_loc};
+  const QkRopeIn ro = {q_norm, k_norm, rope_cos, rope_sin, rope_rows, positions, norm_eps};
+  return decode_impl(p, q, q_tok_stride, k_cache, v_cache, kv_num_pages, indices, cu_k, out,
+                     workspace, workspace_bytes, sm_scale, stream, &nk, &ro);
 }
 
 }  // extern "C"

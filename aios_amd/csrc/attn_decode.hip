@@ -27,9 +27,16 @@
 
 namespace aios {
 
+// The rotation table row of row b (its position clamped into the table);
+// b < 0 (a padding row, whose fragments are zero whatever it reads): row 0.
+__device__ __forceinline__ int64_t decode_rope_row(const DecodeArgs& a, int b) {
+  const int64_t pos = b >= 0 ? (int64_t)a.positions[b] : 0;
+  return min(max(pos, (int64_t)0), a.rope_rows - 1);
+}
+
 // ---------------------------------------------------------------------------
-// prefix part
-template <int D>
+// prefix part (ROPE: the query rows are normalised and rotated on load)
+template <int D, bool ROPE>
 __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArgs& a, int wg) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -57,10 +64,19 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
   const int64_t tok_bytes = a.kv_tok_stride * 2;
   // A wavefront whose 32 rows are all padding only helps stream K/V.
   const bool active = mg * 128 + wave * 32 < a.m_rows;
+  // (rotation on load: the position goes out now, with the page ids)
+  const int64_t rrow = ROPE ? decode_rope_row(a, ok ? b : -1) : 0;
   eng.run(lds, reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2,
           reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2, tok_bytes,
           a.num_pages, a.indices, kv_begin, kv_end, a.scale_log2,
-          [&] { eng.load_q(qr, ok); }, active);
+          [&] {
+            if constexpr (ROPE)
+              eng.load_q_rope(qr, ok, a.q_norm, a.rope_cos + rrow * D, a.rope_sin + rrow * D,
+                              a.norm_eps);
+            else
+              eng.load_q(qr, ok);
+          },
+          active);
 
   if (!ok) return;
   const float l_tot = eng.l_run;
@@ -90,7 +106,7 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
 // rows are the row's query heads.  Each wavefront then writes its own
 // partial state (DecodeArgs::wave_parts), or the four states are merged
 // through LDS by the first wavefront.
-template <int D, int G>
+template <int D, int G, bool ROPE>
 __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArgs& a, int item) {
   using T = KVTile<D>;
   constexpr int CH = T::SUB_BYTES / 16;  // 16-byte chunks per sub-tile (K then V)
@@ -118,8 +134,15 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
 
   TileEngine<D, false, 1> eng;
   eng.reset();
-  eng.load_q_tile(0, a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + min(l16, G - 1)) * D,
-                  l16 < G);
+  // Rotation on load (q_norm given): the row's position goes out now; the
+  // raw fragments, norm weights and cos / sin entries right behind the
+  // first sub-tile's loads (they land with them: no extra memory round
+  // trip, and nothing of them is held while those loads are issued); the
+  // norm and rotation run once they have landed.
+  constexpr bool rope = ROPE;
+  const bf16* qrow = a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + min(l16, G - 1)) * D;
+  const int64_t rrow = rope ? decode_rope_row(a, b) : 0;
+  if (!rope) eng.load_q_tile(0, qrow, l16 < G);
 
   // Fused append: the row's last position is its new token, gathered from
   // k_new / v_new (page selector kNewTok) and written to its page below (no
@@ -141,6 +164,36 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
                           ? reinterpret_cast<const uint8_t*>(a.v_new + (int64_t)b * a.v_new_stride +
                                                              (int64_t)h * D)
                           : g_zero_kv_row;
+  // With the rotation on load, the new token's K row is normalised and
+  // rotated by the wavefront whose sub-tile holds it (lane c < CPR: dims
+  // 8c .. 8c + 7) together with its query rows, written over that
+  // sub-tile's loaded K row once its loads land, and to the cache page at
+  // the end.
+  const bool new_here =
+      t_new >= s_begin && t_new < s_end && ((t_new - s_begin) / kSubTok) % NW == wave;
+  typename TileEngine<D, false, 1>::RopeIn qin;
+  bf16x8 k_x = {}, k_w = {};
+  bf16x8 k_c = {}, k_s = {};
+  auto k_rope = [&]() -> uint4 {
+    constexpr int HALF = T::CPR / 2;
+    const int c = lane & 15;
+    float x[8];
+    unpack_bf16x8(k_x, x);  // zeros past CPR
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+    ss = row16_sum(ss);  // lanes 0 .. 15 hold the row
+    const float inv = rsqrtf(ss / (float)D + a.norm_eps);
+    qk_norm8(x, inv, k_w);
+    const int src = (lane & ~15) + (c < HALF ? c + HALF : c - HALF);
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = __shfl(x[i], src);
+    return lane < T::CPR ? __builtin_bit_cast(uint4, qk_rope8(x, p, c < HALF, k_c, k_s))
+                         : make_uint4(0u, 0u, 0u, 0u);
+  };
+  uint4 knew = make_uint4(0u, 0u, 0u, 0u);
+  bool rope_pending = rope;
   const uint32_t tok_b = (uint32_t)(a.kv_tok_stride * 2);
   const uint32_t n_pages = (uint32_t)a.num_pages;
   int tok_j[NJ];
@@ -181,17 +234,37 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
                                                 : g_zero_kv_row + coff_j[j];
       __builtin_amdgcn_global_load_lds(src, (AIOS_LDS void*)(buf + j * 64 * 16), 16, 0, 0);
     }
+    if (rope_pending) {
+      const bf16* cr = a.rope_cos + rrow * D;
+      const bf16* sr = a.rope_sin + rrow * D;
+      eng.rope_load(qin, qrow, l16 < G, a.q_norm);
+      eng.rope_tables(qin, cr, sr);
+      if (new_here && lane < T::CPR) {
+        k_x = *reinterpret_cast<const bf16x8*>(kn + lane * 16);
+        k_w = *reinterpret_cast<const bf16x8*>(a.k_norm + lane * 8);
+        k_c = *reinterpret_cast<const bf16x8*>(cr + lane * 8);
+        k_s = *reinterpret_cast<const bf16x8*>(sr + lane * 8);
+      }
+    }
     wait_vmcnt<0>();
+    if (rope_pending) {
+      eng.rope_finish(0, qin, l16 < G, a.norm_eps);
+      if (new_here) knew = k_rope();
+      rope_pending = false;
+    }
+    if (rope && new_ok && kv0 <= t_new && t_new < kv0 + kSubTok && lane < T::CPR) {
+      const int tl = t_new - kv0;
+      *reinterpret_cast<uint4*>(buf + tl * T::ROWB + T::k_slot(tl, lane) * 16) = knew;
+    }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     eng.compute(buf, kv0, s_end, a.scale_log2, l16, lg);
   }
   eng.finish();
 
-  if (new_ok && t_new >= s_begin && t_new < s_end &&
-      ((t_new - s_begin) / kSubTok) % NW == wave && lane < 2 * T::CPR) {
+  if (new_ok && new_here && lane < 2 * T::CPR) {
     const bool isv = lane >= T::CPR;
     const int c = isv ? lane - T::CPR : lane;
-    const uint4 v = *reinterpret_cast<const uint4*>((isv ? vn : kn) + c * 16);
+    const uint4 v = (rope && !isv) ? knew : *reinterpret_cast<const uint4*>((isv ? vn : kn) + c * 16);
     *reinterpret_cast<uint4*>(const_cast<uint8_t*>(isv ? vc : kc) + new_dst * tok_b + c * 16) = v;
   }
 
@@ -286,7 +359,7 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   write_rows(acc, l_tot, mx, lds, a.parts.n_chunks + split, a.final_out != 0);
 }
 
-template <int D, int G>
+template <int D, int G, bool ROPE>
 __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_main_kernel(DecodeArgs a) {
   __shared__ __align__(16) uint8_t lds[KVTile<D>::LDS_BYTES];
   // Prefix workgroups first: they carry most of the bytes, and dispatching
@@ -294,9 +367,9 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
   // prefix streaming more than the suffix items gain).
   const int wg = blockIdx.x;
   if (wg < a.prefix_wgs) {
-    decode_prefix_part<D>(lds, a, wg);
+    decode_prefix_part<D, ROPE>(lds, a, wg);
   } else {
-    decode_suffix_item<D, G>(lds, a, wg - a.prefix_wgs);
+    decode_suffix_item<D, G, ROPE>(lds, a, wg - a.prefix_wgs);
   }
 }
 
@@ -431,7 +504,10 @@ static hipError_t launch_main_dg(const DecodeArgs& a, hipStream_t s) {
   const int suffix_wgs = a.suffix_items;
   const dim3 grid(a.prefix_wgs + suffix_wgs);
   if (grid.x == 0) return hipSuccess;
-  hipLaunchKernelGGL((decode_main_kernel<D, G>), grid, dim3(kEngineThreads), 0, s, a);
+  if (a.q_norm != nullptr)
+    hipLaunchKernelGGL((decode_main_kernel<D, G, true>), grid, dim3(kEngineThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_main_kernel<D, G, false>), grid, dim3(kEngineThreads), 0, s, a);
   return hipGetLastError();
 }
 

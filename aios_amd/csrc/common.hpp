@@ -37,6 +37,22 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
 }
 
+// fp32 -> nearest-even bf16 -> fp32.
+__device__ __forceinline__ float round_bf16(float x) {
+  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, static_cast<bf16>(x)) << 16);
+}
+
+// Eight bf16 as fp32, and back (nearest even).
+__device__ __forceinline__ void unpack_bf16x8(const bf16x8& v, float (&f)[8]) {
+  const uint4 u = __builtin_bit_cast(uint4, v);
+  f[0] = lo_bf16(u.x); f[1] = hi_bf16(u.x); f[2] = lo_bf16(u.y); f[3] = hi_bf16(u.y);
+  f[4] = lo_bf16(u.z); f[5] = hi_bf16(u.z); f[6] = lo_bf16(u.w); f[7] = hi_bf16(u.w);
+}
+__device__ __forceinline__ bf16x8 pack_bf16x8(const float (&f)[8]) {
+  return __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]),
+                                               pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])));
+}
+
 // max(a, b) as v_maximum3_f32 (NaN-propagating, so the compiler adds no
 // canonicalising v_max before it as it does for fmaxf; three-input chains
 // fuse).  Inputs here are finite or -inf.

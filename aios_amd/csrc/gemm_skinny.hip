@@ -47,10 +47,6 @@ __device__ __forceinline__ bf16x8 pack8(const float* f) {
                          pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])));
 }
 
-__device__ __forceinline__ float round_bf16(float x) {
-  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, static_cast<bf16>(x)) << 16);
-}
-
 template <int MT, int PRO, int EPI>
 __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a) {
   constexpr int NP = EPI == kSiluPair ? 2 : 1;  // W row sets per workgroup

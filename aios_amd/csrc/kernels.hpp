@@ -65,6 +65,17 @@ struct DecodeArgs {
   int64_t k_new_stride;  // elements per token
   int64_t v_new_stride;
   const int32_t* out_loc;
+  // Per-head q / k RMSNorm + RoPE on load (null q_norm: q and k_new are
+  // final).  q and k_new are then the raw projections; row b is rotated by
+  // the rows of rope_cos / rope_sin [rope_rows][D] (bf16) at positions[b]
+  // (clamped).
+  const bf16* q_norm;
+  const bf16* k_norm;
+  const bf16* rope_cos;
+  const bf16* rope_sin;
+  int64_t rope_rows;
+  const int32_t* positions;
+  float norm_eps;
 };
 
 struct PrefillArgs {

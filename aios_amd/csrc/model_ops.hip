@@ -38,10 +38,6 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
                     pack_bf16x2(f[6], f[7]));
 }
 
-__device__ __forceinline__ float round_bf16(float x) {
-  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, static_cast<bf16>(x)) << 16);
-}
-
 // One workgroup per row.  residual == nullptr: out = rmsnorm(x) * w.
 // Otherwise r = x + residual (fp32), residual <- bf16(r), out = rmsnorm(r) * w.
 // out may alias x: each thread writes only the elements it read.

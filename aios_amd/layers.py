@@ -28,6 +28,11 @@ class HipOps:
     the projections (few-row GEMM kernel for decode-sized inputs, the
     library GEMM for larger ones)."""
 
+    # The decoder may hand an appending decode batch's raw q/k projections to
+    # the attention backend, which applies the q/k RMSNorm + RoPE of
+    # qk_norm_rope inside the decode launch.
+    rope_in_decode = True
+
     @staticmethod
     def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
         rows, k = x.shape

@@ -170,6 +170,54 @@ def append_decode(p: _lib.AttnPlan, q: torch.Tensor, k: torch.Tensor, v: torch.T
     return out
 
 
+def append_decode_rope(p: _lib.AttnPlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       out_loc: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       indices: torch.Tensor, cu_k: torch.Tensor, q_norm: torch.Tensor,
+                       k_norm: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                       positions: torch.Tensor, eps: float, *, out: torch.Tensor | None = None,
+                       workspace: torch.Tensor | None = None,
+                       sm_scale: float | None = None) -> torch.Tensor:
+    """append_decode with the per-head q/k RMSNorm and rotary embedding
+    applied on load (aios_attn_append_decode_rope): q [B, Hq, D] and k
+    [B, Hkv, D] are the raw projections (views into the qkv rows), q_norm /
+    k_norm bf16 [D], cos / sin the fp32 rotary tables rounded to bf16
+    [positions, D], positions int32 [B].  Returns [B, Hq, D] bf16."""
+    if p.phase != _lib.PHASE_DECODE:
+        raise ValueError("plan was not built for decode")
+    _check_q(q, p)
+    if q.shape[0] != p.batch_size:
+        raise ValueError("decode batch must contain one flat token per request")
+    _check_cache(k_cache, p)
+    _check_cache(v_cache, p)
+    _check_i32(indices, "indices", p.total_kv)
+    _check_i32(cu_k, "cu_k", p.batch_size + 1)
+    _check_new_kv(k, v, out_loc, p)
+    for w, name in ((q_norm, "q_norm"), (k_norm, "k_norm")):
+        if w.dtype != torch.bfloat16 or w.numel() != p.head_dim or not w.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous bfloat16 [head_dim] tensor")
+    if (cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16 or cos.shape != sin.shape
+            or cos.ndim != 2 or cos.shape[1] != p.head_dim or not cos.is_contiguous()
+            or not sin.is_contiguous()):
+        raise ValueError("cos/sin tables must be contiguous bfloat16 [positions, head_dim]")
+    _check_i32(positions, "positions", p.batch_size)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if p.ws_bytes and (workspace is None or workspace.numel() < p.ws_bytes):
+        raise RuntimeError(f"decode needs a workspace of {p.ws_bytes} bytes")
+    scale = p.head_dim ** -0.5 if sm_scale is None else sm_scale
+    _lib.check(
+        _lib.lib().aios_attn_append_decode_rope(
+            p, q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
+            out_loc.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
+            indices.data_ptr(), cu_k.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(),
+            cos.data_ptr(), sin.data_ptr(), cos.shape[0], positions.data_ptr(), float(eps),
+            out.data_ptr(), workspace.data_ptr() if workspace is not None else None,
+            workspace.numel() if workspace is not None else 0, scale, _stream(q.device)),
+        "aios_attn_append_decode_rope",
+    )
+    return out
+
+
 def prefill(p: _lib.AttnPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
             indices: torch.Tensor, cu_q: torch.Tensor, cu_k: torch.Tensor, *,
             out: torch.Tensor | None = None, sm_scale: float | None = None) -> torch.Tensor:

@@ -75,7 +75,9 @@ def weights_to(w: dict, device, dtype=None) -> dict:
 
 
 class RotaryEmbedding:
-    """fp32 cos/sin tables [max_positions, head_dim] (rotary.py:8-29)."""
+    """fp32 cos/sin tables [max_positions, head_dim] (rotary.py:8-29), and
+    the same rounded to bf16 (nearest even: the rounding the q/k rotation
+    applies to each entry) for the decode launch that rotates on load."""
 
     def __init__(self, head_dim: int, max_positions: int, base: float, device) -> None:
         inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
@@ -83,6 +85,8 @@ class RotaryEmbedding:
         emb = torch.cat((torch.outer(t, inv_freq),) * 2, dim=-1)
         self.cos = emb.cos().to(device)
         self.sin = emb.sin().to(device)
+        self.cos_bf16 = self.cos.to(torch.bfloat16)
+        self.sin_bf16 = self.sin.to(torch.bfloat16)
 
 
 class Qwen3ForCausalLM:
@@ -112,15 +116,26 @@ class Qwen3ForCausalLM:
     def _attention(self, i: int, qkv: torch.Tensor, positions, kv_cache, batch) -> torch.Tensor:
         """qwen3.py:52-75 after the qkv projection: per-head q/k RMSNorm +
         RoPE, the backend, o_proj (v stays a strided view into qkv, as in the
-        reference)."""
+        reference).  An appending decode batch on the gfx950 ops takes the
+        norm and rotation inside the decode launch (forward_rope)."""
         c = self.config
         lw = self.w["layers"][i]
         t = qkv.shape[0]
-        q, k = self.ops.qk_norm_rope(qkv, lw["q_norm"], lw["k_norm"], self.rotary.cos,
-                                     self.rotary.sin, positions, c.num_qo_heads, c.num_kv_heads,
-                                     c.head_dim, c.rms_norm_eps)
-        v = qkv[:, self._q_size + self._kv_size:].view(t, c.num_kv_heads, c.head_dim)
-        out = self.attn_backend.forward(q, k, v, kv_cache, i, batch)
+        hq, hkv, d = c.num_qo_heads, c.num_kv_heads, c.head_dim
+        v = qkv[:, self._q_size + self._kv_size:].view(t, hkv, d)
+        be = self.attn_backend
+        if (getattr(self.ops, "rope_in_decode", False)
+                and getattr(be, "decode_rope_applies", None) is not None
+                and be.decode_rope_applies(batch)):
+            q = qkv[:, :self._q_size].view(t, hq, d)
+            k = qkv[:, self._q_size:self._q_size + self._kv_size].view(t, hkv, d)
+            out = be.forward_rope(q, k, v, lw["q_norm"], lw["k_norm"], self.rotary.cos_bf16,
+                                  self.rotary.sin_bf16, positions, c.rms_norm_eps, kv_cache, i,
+                                  batch)
+        else:
+            q, k = self.ops.qk_norm_rope(qkv, lw["q_norm"], lw["k_norm"], self.rotary.cos,
+                                         self.rotary.sin, positions, hq, hkv, d, c.rms_norm_eps)
+            out = be.forward(q, k, v, kv_cache, i, batch)
         return self.ops.linear(out.reshape(t, -1), lw["o"])
 
     def forward(self) -> torch.Tensor:

@@ -23,6 +23,9 @@
  *                      attention/flashinfer.py:374-394)
  *   aios_attn_append_decode  store_kv (flashinfer.py:389 -> store.py:32-61)
  *                      and the decode run above, in one launch
+ *   aios_attn_append_decode_rope  the same with Qwen3Attention's q/k norm
+ *                      and rotary embedding (python/aios/models/qwen3.py:
+ *                      52-67) applied on load
  *   aios_build_indices the device half of prepare_metadata's
  *                      torch.cat([page_table[row, :device_len] ...])
  *                      (python/aios/attention/flashinfer.py:228-230)
@@ -207,6 +210,36 @@ int aios_attn_append_decode(const aios_attn_plan_t* plan, const void* q,
                             const int32_t* indices, const int32_t* cu_k,
                             void* out, void* workspace, int64_t workspace_bytes,
                             float sm_scale, void* stream);
+
+/*
+ * aios_attn_append_decode with the per-head query/key RMSNorm and rotary
+ * embedding of the decoder layer applied on load: q and k_new are the raw
+ * projections (the q and k parts of the fused qkv rows), and the result -
+ * attention output and the K row written to page out_loc[b] - is that of
+ *   aios_qk_norm_rope(q/k rows, q_norm, k_norm, cos, sin, rope_rows,
+ *                     positions, norm_eps)
+ * followed by aios_attn_append_decode on its outputs (the fp32 sum of squares
+ * of a head is taken in another order, so a normalised element can differ by
+ * one bf16 unit where that sum rounds differently).  Replaces, for a decode
+ * batch, the q_norm / k_norm + rotary embedding of Qwen3Attention.forward
+ * (python/aios/models/qwen3.py:52-67) together with store_kv and the decode
+ * run (python/aios/attention/flashinfer.py:374-394).  q_norm, k_norm: bf16
+ * [D]; rope_cos, rope_sin: bf16 [rope_rows][D], the fp32 cos / sin tables
+ * of aios_qk_norm_rope rounded to bf16 (nearest even: the rounding that
+ * call applies to each entry it uses); positions: int32 [batch_size]
+ * (clamped into the table); these and the k_new rows 16-byte aligned.
+ */
+int aios_attn_append_decode_rope(const aios_attn_plan_t* plan, const void* q,
+                                 int64_t q_tok_stride, const void* k_new,
+                                 int64_t k_tok_stride, const void* v_new,
+                                 int64_t v_tok_stride, const int32_t* out_loc,
+                                 void* k_cache, void* v_cache, int64_t kv_num_pages,
+                                 const int32_t* indices, const int32_t* cu_k,
+                                 const void* q_norm, const void* k_norm,
+                                 const void* rope_cos, const void* rope_sin,
+                                 int64_t rope_rows, const int32_t* positions,
+                                 float norm_eps, void* out, void* workspace,
+                                 int64_t workspace_bytes, float sm_scale, void* stream);
 
 /*
  * aios_attn_decode without a workspace argument, for callers that cannot

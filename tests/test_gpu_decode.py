@@ -270,6 +270,99 @@ def test_append_decode_matches_separate_calls(case):
         _append_decode_case(OP_TEST, 9, shared=0)
 
 
+def _append_decode_rope_case(shape, seed, shared=None, chunk=0, split=0):
+    """aios_attn_append_decode_rope against aios_qk_norm_rope followed by
+    aios_attn_append_decode on the same raw qkv rows: V rows bitwise equal;
+    each new K element equal or one bf16 unit apart (the head's fp32 sum of
+    squares is taken in another order) and almost all equal; attention
+    outputs within the bf16 tolerance of the separate path's and of the
+    float64 oracle over the fused path's cache."""
+    from aios_amd.layers import HipOps
+    from aios_amd.qwen3 import RotaryEmbedding
+
+    wl = make_decode_workload(shape, seed=seed, extra_token=True)
+    n, hq, hkv, d = shape.num_rows, shape.num_qo_heads, shape.num_kv_heads, shape.head_dim
+    g = torch.Generator().manual_seed(seed + 7)
+    qkv = torch.randn(n, (hq + 2 * hkv) * d, generator=g).to(torch.bfloat16).to(DEV)
+    qw = (1.0 + 0.2 * torch.randn(d, generator=g)).to(torch.bfloat16).to(DEV)
+    kw = (1.0 + 0.2 * torch.randn(d, generator=g)).to(torch.bfloat16).to(DEV)
+    rot = RotaryEmbedding(d, 8192, 1e6, DEV)
+    kv_len = (wl.cu_k[1:] - wl.cu_k[:-1]).to(torch.int32)
+    positions = (kv_len - 1).to(DEV)
+    eps = 1e-6
+    last = torch.tensor([int(wl.indices[int(wl.cu_k[i + 1]) - 1]) for i in range(n)],
+                        dtype=torch.int32)
+    out_loc = last.to(DEV)
+    cu_q = torch.arange(n + 1, dtype=torch.int32)
+    p = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d,
+                   shared_prefix_len=shape.prefix_len if shared is None else shared,
+                   workspace_bytes=64 << 20, prefix_chunk_len=chunk, suffix_split_len=split)
+    ws = torch.empty(max(p.ws_bytes, 256), dtype=torch.uint8, device=DEV)
+    idx = wl.indices.to(DEV)
+    cuk = wl.cu_k.to(DEV)
+    v = qkv[:, (hq + hkv) * d:].view(n, hkv, d)
+    # separate: q/k norm + rotation, then append + decode
+    q_a, k_a = HipOps.qk_norm_rope(qkv, qw, kw, rot.cos, rot.sin, positions, hq, hkv, d, eps)
+    ka, va = wl.k_cache[0].to(DEV), wl.v_cache[0].to(DEV)
+    out_a = paged.append_decode(p, q_a, k_a, v, out_loc, ka, va, idx, cuk, workspace=ws)
+    # one launch from the raw projections
+    q_raw = qkv[:, :hq * d].view(n, hq, d)
+    k_raw = qkv[:, hq * d:(hq + hkv) * d].view(n, hkv, d)
+    kb, vb = wl.k_cache[0].to(DEV), wl.v_cache[0].to(DEV)
+    out_b = paged.append_decode_rope(p, q_raw, k_raw, v, out_loc, kb, vb, idx, cuk, qw, kw,
+                                     rot.cos_bf16, rot.sin_bf16, positions, eps, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(bits_t(va), bits_t(vb))
+    rest = torch.ones(ka.shape[0], dtype=torch.bool)
+    rest[last.long()] = False
+    assert torch.equal(bits_t(ka[rest.to(DEV)]), bits_t(kb[rest.to(DEV)]))
+    new_a, new_b = ka[out_loc.long()].float(), kb[out_loc.long()].float()
+    # one unit of the normalised element moves the rotated one by at most
+    # about one unit of the head's largest element
+    scale = new_a.abs().amax(dim=-1, keepdim=True)
+    assert bool(((new_a - new_b).abs() <= scale * 2.0 ** -6).all())
+    assert float((new_a == new_b).float().mean()) > 0.97
+    np.testing.assert_allclose(to_np64(out_b), to_np64(out_a), **BF16_TOL)
+    ref = oatt.decode_attention(to_np64(q_a), to_np64(kb), to_np64(vb), wl.indices.numpy(),
+                                wl.cu_k.numpy(), d ** -0.5)
+    np.testing.assert_allclose(to_np64(out_b), ref, **BF16_TOL)
+    return p
+
+
+@pytest.mark.parametrize("case", ["op_test", "cascade", "splits", "long_context_layer",
+                                  "h64_g3", "h128_g2", "h64_cascade", "h128_cascade"])
+def test_append_decode_rope_matches_separate_ops(case):
+    """The q/k norm + rotary embedding taken inside the decode launch, for
+    both tile engines (prefix cascade: 32-row tiles; suffix items: 16-row
+    tiles) at head sizes 64, 96 and 128."""
+    if case == "op_test":
+        p = _append_decode_rope_case(OP_TEST, 20260814)
+        assert p.prefix_len == 0
+    elif case == "cascade":
+        p = _append_decode_rope_case(OP_TEST, 3, chunk=32)
+        assert p.prefix_len == 24
+    elif case == "splits":
+        p = _append_decode_rope_case(DecodeShape("sp", 1, 8, 200, 40, 8, 2, 96, 1024), 11,
+                                     chunk=64, split=8)
+        assert p.num_suffix_splits > 1
+    elif case == "long_context_layer":
+        shape = DecodeShape("lc1", 1, 24, 4096, 64, 32, 8, 128, 65536)
+        p = _append_decode_rope_case(shape, 20260814)
+        assert p.num_prefix_chunks > 1
+    elif case == "h64_g3":
+        _append_decode_rope_case(DecodeShape("h64", 1, 8, 150, 20, 12, 4, 64, 512), 5, shared=0)
+    elif case == "h128_g2":
+        _append_decode_rope_case(DecodeShape("h128", 1, 8, 140, 24, 16, 8, 128, 512), 6, shared=0)
+    elif case == "h64_cascade":
+        p = _append_decode_rope_case(DecodeShape("h64c", 1, 8, 150, 20, 12, 4, 64, 512), 5,
+                                     chunk=64)
+        assert p.prefix_len == 150
+    else:
+        p = _append_decode_rope_case(DecodeShape("h128c", 1, 8, 140, 24, 16, 8, 128, 512), 6,
+                                     chunk=64)
+        assert p.prefix_len == 140
+
+
 def test_append_decode_out_of_range_slot_matches_separate_calls():
     _append_decode_case(OP_TEST, 4, chunk=32, oob_row=3)
 

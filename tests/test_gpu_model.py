@@ -152,6 +152,40 @@ def _check_candidate_group(eng, om, prefix, n, steps):
     return res
 
 
+def test_candidate_group_h64_norm_rope_in_decode():
+    """Head size 64 (the MiniMind-IME 0.1B shape, 4 layers): the decode steps
+    take the q/k norm + rotation inside the decode launch; every eager step's
+    logits against the oracle, then graph-replayed groups token for token
+    equal to the eager ones."""
+    c = MINIMIND_IME_0P1B.with_layers(4)
+    eng, om = _engine(c, 11)
+    be = eng.rt.model.attn_backend
+    assert c.head_dim in be.ROPE_IN_DECODE_HEAD_DIMS
+    calls = []
+    inner = be.forward_rope
+
+    def counted(*args, **kw):
+        calls.append(1)
+        return inner(*args, **kw)
+
+    be.forward_rope = counted
+    prefix = _prefix(11, 20, c.vocab_size)
+    _check_candidate_group(eng, om, prefix, 8, 10)
+    assert len(calls) == c.num_layers * 9  # every decode step after the first token
+    eng.reset_prefix_cache()
+    graphed = CandidateGroupEngine(eng.rt, use_graphs=True)
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=10)
+    for _ in range(2):
+        e = eng.complete(prefix, cfg)
+        eng.reset_prefix_cache()
+        torch.cuda.synchronize()
+        g = graphed.complete(prefix, cfg)
+        graphed.reset_prefix_cache()
+        assert [x.token_ids for x in g.raw_candidates] == [x.token_ids for x in e.raw_candidates]
+        assert [x.average_logprob for x in g.raw_candidates] == \
+            [x.average_logprob for x in e.raw_candidates]
+
+
 def test_candidate_group_minimind_0p1b():
     """Prefill a 32-token prefix, 8 candidates x 16 greedy steps over shared prefix KV."""
     c = MINIMIND_0P1B
