@@ -367,9 +367,10 @@ def test_oracle_model_matches_product_decoder_composition():
 
     c = _tiny_config(num_layers=3)
     w = init_weights(c, 1, "cpu", dtype=torch.float32, std=0.2)
+    g = torch.Generator().manual_seed(3)
     for lw in w["layers"]:  # non-trivial norm weights
         for key in ("input_norm", "post_norm", "q_norm", "k_norm"):
-            lw[key].uniform_(0.5, 1.5)
+            lw[key].uniform_(0.5, 1.5, generator=g)
     ids = torch.tensor([5, 9, 2, 44, 0, 13])
     backend = _DenseCpuBackend(c.head_dim ** -0.5)
     from tests.util import TorchOps
@@ -534,10 +535,11 @@ def test_oracle_attnres_model_matches_product_composition():
 
     c = _tiny_attnres()
     w = init_weights(c, 2, "cpu", dtype=torch.float32, std=0.2)
+    g = torch.Generator().manual_seed(3)
     for lw in w["layers"]:
         for key in ("input_norm", "post_norm", "q_norm", "k_norm", "attn_res_norm",
                     "mlp_res_norm"):
-            lw[key].uniform_(0.5, 1.5)
+            lw[key].uniform_(0.5, 1.5, generator=g)
         lw["attn_res_query"].mul_(20.0)  # routing far from uniform
         lw["mlp_res_query"].mul_(20.0)
     w["final_res_query"].mul_(20.0)
