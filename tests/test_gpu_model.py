@@ -240,6 +240,46 @@ def test_lcp_extension_and_strict_backspace():
     assert eng.rt.cache_manager.available_size == eng.rt.num_pages - 128
 
 
+def test_qwen3_0p6b_full_size_extension_and_decode():
+    """The Qwen3-0.6B shape at full size (28 layers, 16q/8kv heads of 128,
+    vocab 151,936): a 128-token prefix, its 2-token LCP extension prefilled
+    against the cached prefix KV, then 8 candidates x 3 eager decode steps
+    over the shared 130-token prefix (the cascade).  The extension's
+    last-position logits, the first-token ranking, and two candidates' every
+    decode step against the float32 oracle."""
+    c = QWEN3_0P6B
+    eng, om = _engine(c, 3)
+    base = _prefix(3, 128, c.vocab_size)
+    ext = base + _prefix(4, 2, c.vocab_size)
+    cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=3)
+    eng.complete(base, cfg)
+    rec = _record_decode_logits(eng)
+    res = eng.complete(ext, cfg)
+    assert res.reused_prefix_tokens == 128 and res.active_model_tokens == 2 + 8 * 2
+    ref0 = om.logits(torch.tensor(ext)[None], 129)[0, -1].log_softmax(-1)
+    gpu0 = res.prefix_logits[0].float().cpu().log_softmax(-1)
+    d0 = (gpu0 - ref0).abs().max().item()
+    assert d0 <= LOGIT_TOL_TIGHT, d0
+    ids = torch.tensor([x.token_ids for x in res.raw_candidates])
+    assert ids.shape == (8, 3)
+    # candidate i starts from the GPU's i-th best first token; under the
+    # oracle each is within 2 * d0 of the oracle's i-th best
+    top_vals = ref0.sort(descending=True).values[:8]
+    assert (ref0[ids[:, 0]] - top_vals).abs().max().item() <= 2 * d0 + 1e-6
+    assert len(rec) == 2
+    for r in (0, 5):
+        seq = torch.tensor(ext + ids[r, :2].tolist())
+        ref_r = om.logits(seq[None], len(ext))[0].log_softmax(-1)  # next-token at 130, 131
+        for j, (rows, logits) in enumerate(rec):
+            lp = logits[rows.index(r)].log_softmax(-1)
+            dev = (lp - ref_r[j]).abs().max().item()
+            assert dev <= LOGIT_TOL_TIGHT, (r, j, dev)
+            tok = ids[r, j + 1]
+            assert tok.item() == lp.argmax().item()
+            assert (ref_r[j].max() - ref_r[j][tok]).item() <= 2 * dev + 1e-6, (r, j)
+    assert eng.rt.cache_manager.available_size == eng.rt.num_pages - 130
+
+
 def test_cancelled_and_budget():
     c = MINIMIND_0P1B.with_layers(2)
     eng, _ = _engine(c, 1, num_pages=256)
