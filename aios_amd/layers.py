@@ -66,20 +66,28 @@ class HipOps:
         (activation.py:9-12)."""
         rows, k = h.shape
         n = weight.shape[0] // 2 if silu else weight.shape[0]
-        if self._rows_ok(h, weight, k) and n % 16 == 0 and \
-                ((k // 4) // 32) * ((rows + 15) // 16) <= 8 and \
+        # The prologue keeps (K/128) x (16-row tiles) normalised fragments in
+        # registers, at most 8: more rows than one launch holds run as row
+        # chunks (each re-reading the weights, mostly from L2) rather than
+        # as separate norm, projection and activation launches.
+        frags = (k // 4) // 32
+        chunk = 16 * (8 // frags) if 1 <= frags <= 8 else 0
+        if chunk and self._rows_ok(h, weight, k) and n % 16 == 0 and \
                 (residual is None or (residual.stride(1) == 1 and residual.stride(0) % 8 == 0)):
             y = torch.empty(rows, n, dtype=h.dtype, device=h.device)
             new_res = torch.empty_like(h) if residual is not None else h
-            _lib.check(_lib.lib().aios_linear_rows_ex(
-                h.data_ptr(), h.stride(0), weight.data_ptr(), weight.stride(0), y.data_ptr(),
-                y.stride(0), rows, n, k, _lib.PROLOGUE_ADD_RMSNORM,
-                residual.data_ptr() if residual is not None else None,
-                residual.stride(0) if residual is not None else 0, norm_weight.data_ptr(), eps,
-                new_res.data_ptr() if residual is not None else None,
-                new_res.stride(0) if residual is not None else 0,
-                _lib.EPILOGUE_SILU_MUL if silu else _lib.EPILOGUE_NONE, _stream(h)),
-                "aios_linear_rows_ex")
+            lib = _lib.lib()
+            for r0 in range(0, rows, chunk):
+                m = min(chunk, rows - r0)
+                _lib.check(lib.aios_linear_rows_ex(
+                    h[r0:].data_ptr(), h.stride(0), weight.data_ptr(), weight.stride(0),
+                    y[r0:].data_ptr(), y.stride(0), m, n, k, _lib.PROLOGUE_ADD_RMSNORM,
+                    residual[r0:].data_ptr() if residual is not None else None,
+                    residual.stride(0) if residual is not None else 0, norm_weight.data_ptr(),
+                    eps, new_res[r0:].data_ptr() if residual is not None else None,
+                    new_res.stride(0) if residual is not None else 0,
+                    _lib.EPILOGUE_SILU_MUL if silu else _lib.EPILOGUE_NONE, _stream(h)),
+                    "aios_linear_rows_ex")
             return y, new_res
         if residual is None:
             x, residual = self.rmsnorm(h, norm_weight, eps), h

@@ -97,11 +97,14 @@ def test_linear_rows_strided_input_and_fallback():
 
 
 @pytest.mark.parametrize("rows,k,n", [(1, 768, 1152), (8, 768, 1152), (8, 768, 6400),
-                                      (24, 1024, 512), (40, 512, 256), (8, 2048, 768)])
+                                      (24, 1024, 512), (40, 512, 256), (8, 2048, 768),
+                                      (24, 768, 1152), (17, 768, 1152)])
 @pytest.mark.parametrize("with_residual", [True, False])
 def test_add_rmsnorm_linear(rows, k, n, with_residual):
     """RMSNorm (with the residual add) folded into the projection: the same
-    normalised operand as the separate kernels, the residual sum bit-exact."""
+    normalised operand as the separate kernels, the residual sum bit-exact;
+    more rows than one launch holds (17, 24 at K 768 / 1024; 40 at K 512)
+    run as row chunks."""
     h = _bf16((rows, k), rows + k, 2.0)
     r = _bf16((rows, k), rows + k + 1, 3.0) if with_residual else None
     nw = _bf16((k,), 9).abs() + 0.5
@@ -120,7 +123,7 @@ def test_add_rmsnorm_linear(rows, k, n, with_residual):
 
 
 @pytest.mark.parametrize("rows,k,inter", [(8, 768, 2048), (3, 512, 256), (33, 256, 512),
-                                          (1, 1024, 3072)])
+                                          (1, 1024, 3072), (24, 768, 2048), (24, 1024, 3072)])
 @pytest.mark.parametrize("with_residual", [True, False])
 def test_add_rmsnorm_linear_silu_pair(rows, k, inter, with_residual):
     """Norm folded in front of the merged gate/up projection and SiLU-and-mul
