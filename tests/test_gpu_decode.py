@@ -411,3 +411,23 @@ def test_misaligned_output_is_rejected():
     with pytest.raises(ValueError, match="16-byte aligned"):
         paged.decode(p, wl.q[0].to(DEV), wl.k_cache[0].to(DEV), wl.v_cache[0].to(DEV),
                      wl.indices.to(DEV), wl.cu_k.to(DEV), out=bad, workspace=ws)
+
+
+def test_empty_batches_are_noops():
+    """A batch with no requests: decode and prefill plans carry no work, and
+    the calls return empty outputs without touching the caches."""
+    cu = torch.zeros(1, dtype=torch.int32)
+    kc = torch.randn(16, 2, 96, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(16, 2, 96, device=DEV).to(torch.bfloat16)
+    k0, v0 = kc.clone(), vc.clone()
+    idx = torch.zeros(0, dtype=torch.int32, device=DEV)
+    q = torch.zeros(0, 8, 96, dtype=torch.bfloat16, device=DEV)
+    pd = paged.plan("decode", cu, cu, 8, 2, 96)
+    assert pd.batch_size == 0 and pd.ws_bytes == 0
+    out = paged.decode(pd, q, kc, vc, idx, cu.to(DEV))
+    pp = paged.plan("prefill", cu, cu, 8, 2, 96)
+    assert pp.num_q_tiles == 0
+    out2 = paged.prefill(pp, q, kc, vc, idx, cu.to(DEV), cu.to(DEV))
+    torch.cuda.synchronize()
+    assert out.shape == (0, 8, 96) and out2.shape == (0, 8, 96)
+    assert torch.equal(kc, k0) and torch.equal(vc, v0)
