@@ -47,7 +47,9 @@ __device__ __forceinline__ bf16x8 pack8(const float* f) {
                          pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])));
 }
 
-template <int MT, int PRO, int EPI>
+// KS > 0: the K steps of a wavefront (K / 128) fixed at compile time, so
+// the operand loads are one straight-line burst; KS = 0: read from K.
+template <int MT, int PRO, int EPI, int KS = 0>
 __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a) {
   constexpr int NP = EPI == kSiluPair ? 2 : 1;  // W row sets per workgroup
   __shared__ f32x4 red[3][NP][MT][64];
@@ -59,7 +61,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
   const int64_t n0 = (int64_t)blockIdx.x * 16;
   const int kq = a.K >> 2;  // multiple of 32
   const int k_begin = wave * kq + lg * 8;
-  const int steps = kq >> 5;
+  const int steps = KS > 0 ? KS : kq >> 5;
   const bf16* wrow[NP];
   wrow[0] = a.w + (n0 + l16) * a.w_stride + k_begin;
   if constexpr (NP == 2) wrow[NP - 1] = a.w + (a.N + n0 + l16) * a.w_stride + k_begin;
@@ -275,6 +277,20 @@ __global__ __launch_bounds__(64) void skinny_gemm_cols_kernel(LinearArgs a) {
 template <int PRO, int EPI>
 hipError_t launch_pe(const LinearArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)(a.N / 16));
+  if ((a.M + 15) / 16 == 1) {
+    // the decode-step shapes: K = 768, 1024, 2048 (one 16-row tile)
+    switch (a.K / 128) {
+      case 6: hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 6>), grid, dim3(kGemmThreads), 0, stream, a); return hipGetLastError();
+      case 8: hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 8>), grid, dim3(kGemmThreads), 0, stream, a); return hipGetLastError();
+      case 16:
+        if constexpr (PRO == kPlain) {
+          hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 16>), grid, dim3(kGemmThreads), 0, stream, a);
+          return hipGetLastError();
+        }
+        break;
+      default: break;
+    }
+  }
   switch ((a.M + 15) / 16) {
     case 1: hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI>), grid, dim3(kGemmThreads), 0, stream, a); break;
     case 2: hipLaunchKernelGGL((skinny_gemm_kernel<2, PRO, EPI>), grid, dim3(kGemmThreads), 0, stream, a); break;
