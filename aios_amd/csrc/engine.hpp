@@ -55,6 +55,14 @@ static __device__ __align__(16) uint8_t g_zero_kv_row[512] = {0};
 
 // Word 3 of a raw buffer descriptor on gfx9-family GPUs (32-bit data format).
 constexpr int kBufferWord3 = 0x00020000;
+// Cache policy of a buffer load: NT, the non-temporal (streaming) hint.
+// The shared-prefix gathers of a decode read each prefix KV row once per
+// launch; marked streaming they leave the caches to what the next launch
+// reads again (page ids, query rows, partial states).  The per-row suffix
+// gathers keep the default policy (a CandidateGroup step re-reads its
+// rows' short KV every step, and measured slower streamed), and so does
+// the prefill (the query tiles of one kv-head re-read its K/V from L2).
+constexpr int kCpolStream = 2;
 
 // s_waitcnt with vmcnt <= N and the other counters unconstrained.
 template <int N>
@@ -191,7 +199,8 @@ __device__ __forceinline__ bf16x8 qk_rope8(const float (&xn)[8], const float (&p
 // `math(sb, kv0)` runs one sub-tile's math (ring slot at byte offset sb,
 // positions kv0 ..) and is skipped when `active` is false (a wavefront whose
 // rows are all padding only helps stream).
-template <class T, typename QLoad, typename Math>
+// CPOL: cache policy of the gathers.
+template <class T, int CPOL, typename QLoad, typename Math>
 __device__ __forceinline__ void stream_kv(uint8_t* lds, const uint8_t* kc, const uint8_t* vc,
                                           int64_t tok_bytes, int64_t num_pages, const int32_t* idx,
                                           int kv_begin, int kv_end, QLoad&& qload, Math&& math,
@@ -282,7 +291,7 @@ __device__ __forceinline__ void stream_kv(uint8_t* lds, const uint8_t* kc, const
       const uint32_t off = __umul24(min(page[j], n_pages), tok_b) + coff_j[j];
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           isv_j[j] ? rv : rk, (AIOS_LDS void*)(buf + (j * kEngineThreads + wave_u * 64) * 16),
-          16, off, 0, 0, 0);
+          16, off, 0, 0, CPOL);
     }
   };
 
@@ -707,9 +716,11 @@ struct TileEngine32 {
                       float scale_log2, QLoad&& qload, bool active = true) {
     reset();
     const LaneOff lo = lane_offsets(lds);
-    stream_kv<T>(lds, kc, vc, tok_bytes, num_pages, idx, kv_begin, kv_end, qload,
-                 [&](uint32_t sb, int kv0) { compute_at(lo, sb, kv0, kv_end, scale_log2); },
-                 active);
+    // The causal (prefill) engine re-reads K/V across query tiles; the
+    // decode engine (shared prefix) streams it once.
+    stream_kv<T, CAUSAL ? 0 : kCpolStream>(
+        lds, kc, vc, tok_bytes, num_pages, idx, kv_begin, kv_end, qload,
+        [&](uint32_t sb, int kv0) { compute_at(lo, sb, kv0, kv_end, scale_log2); }, active);
     l_run = ol[0];
   }
 
