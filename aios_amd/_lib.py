@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "aios_qk_norm_rope",
     "aios_cg_step_begin",
     "aios_cg_step_end",
+    "aios_cg_step_prepare",
     "aios_silu_mul",
     "aios_linear_rows",
     "aios_linear_rows_ex",
@@ -143,6 +144,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.aios_rmsnorm.argtypes = [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i32, _f32, _vp]
     lib.aios_cg_step_begin.restype = ctypes.c_int
     lib.aios_cg_step_begin.argtypes = [_vp, _vp, _i32, _i32, _vp, _vp, _i64, _i32, _vp, _vp]
+    lib.aios_cg_step_prepare.restype = ctypes.c_int
+    lib.aios_cg_step_prepare.argtypes = [_vp, _vp, _i32, _i32, _vp, _vp, _i64, _i32, _vp, _vp,
+                                         _vp, _i32, _vp, _vp, _vp, _i64, _i32, _vp, _vp]
     lib.aios_cg_step_end.restype = ctypes.c_int
     lib.aios_cg_step_end.argtypes = [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _vp,
                                      _vp, _vp, _vp, _vp, _vp]

@@ -17,7 +17,7 @@ from __future__ import annotations
 
 from contextlib import contextmanager
 from dataclasses import dataclass, field
-from typing import TYPE_CHECKING, List, Literal
+from typing import TYPE_CHECKING, List, Literal, Optional
 
 import torch
 
@@ -88,6 +88,9 @@ class Batch:
     return_all_logits: bool = False
     shared_prefix_len: int = 0
     fused_append: bool = False
+    # The rows' embeddings when the caller has gathered them already (a
+    # captured CandidateGroup step does it with its step preparation).
+    input_embeds: Optional[torch.Tensor] = None
 
     @property
     def is_prefill(self) -> bool:

@@ -659,6 +659,50 @@ int aios_cg_step_begin(int64_t* step, const int32_t* pages, int32_t page_rows, i
   return check_hip(aios::cg_step_begin(a, static_cast<hipStream_t>(stream)), "cg_step_begin launch");
 }
 
+int aios_cg_step_prepare(int64_t* step, const int32_t* pages, int32_t page_rows, int32_t rows,
+                         int32_t* out_loc, int32_t* page_table, int64_t pt_stride, int32_t pt_cols,
+                         int32_t* pos, int32_t* cu_k, int32_t* indices, int32_t max_kv_len,
+                         int64_t* step_next, const int64_t* tokens, const void* embed,
+                         int64_t vocab, int32_t hidden, void* h_out, void* stream) {
+  if (rows <= 0 || page_rows <= 0 || pt_cols <= 0 || pt_stride < pt_cols)
+    return fail(AIOS_ERR_INVALID, "cg_step_prepare: bad sizes");
+  if (max_kv_len <= 0 || max_kv_len > pt_cols)
+    return fail(AIOS_ERR_INVALID, "cg_step_prepare: max_kv_len %d outside [1, %d]", max_kv_len,
+                pt_cols);
+  if (!step || !pages || !out_loc || !page_table || !pos || !cu_k || !indices)
+    return fail(AIOS_ERR_INVALID, "cg_step_prepare: null pointer");
+  if (embed) {
+    if (!tokens || !h_out) return fail(AIOS_ERR_INVALID, "cg_step_prepare: null pointer");
+    if (vocab <= 0 || hidden <= 0 || (hidden % 8) != 0)
+      return fail(AIOS_ERR_INVALID, "cg_step_prepare: embedding of %lld x %d (hidden must be a "
+                                    "positive multiple of 8)", (long long)vocab, hidden);
+    if ((((uintptr_t)embed | (uintptr_t)h_out) & 15) != 0)
+      return fail(AIOS_ERR_INVALID, "cg_step_prepare: embedding table and rows must be 16-byte "
+                                    "aligned");
+  }
+  aios::CgStepArgs a = {};
+  a.rows = rows;
+  a.step = step;
+  a.pages = pages;
+  a.page_rows = page_rows;
+  a.out_loc = out_loc;
+  a.page_table = page_table;
+  a.pt_stride = pt_stride;
+  a.pt_cols = pt_cols;
+  a.pos = pos;
+  a.cu_k = cu_k;
+  a.indices = indices;
+  a.max_kv_len = max_kv_len;
+  a.step_next = step_next;
+  a.tokens = const_cast<int64_t*>(tokens);
+  a.embed = static_cast<const aios::bf16*>(embed);
+  a.vocab = vocab;
+  a.hidden = hidden;
+  a.h_out = static_cast<aios::bf16*>(h_out);
+  return check_hip(aios::cg_step_prepare(a, static_cast<hipStream_t>(stream)),
+                   "cg_step_prepare launch");
+}
+
 int aios_cg_step_end(int64_t* step, int32_t rows, const int64_t* tok, const float* raw, int64_t eos,
                      uint8_t* finished, uint8_t* eos_hit, int64_t* out_ids, int64_t out_stride,
                      int32_t out_cols, float* logp_sum, int64_t* counts, int64_t* tokens,

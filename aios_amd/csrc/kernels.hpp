@@ -163,8 +163,18 @@ struct CgStepArgs {
   int64_t* counts;          // [rows]
   int64_t* tokens;          // [rows] next input ids
   int64_t* fed;             // [1] live rows fed so far
+  // cg_step_prepare: the step's decode metadata and inputs
+  int32_t* cu_k;            // [rows + 1]
+  int32_t* indices;         // [rows * max_kv_len]
+  int32_t max_kv_len;
+  int64_t* step_next;       // [1] *step + 1 (may be null)
+  const bf16* embed;        // [vocab][hidden] (null: no embedding gather)
+  int64_t vocab;
+  int32_t hidden;
+  bf16* h_out;              // [rows][hidden]
 };
 hipError_t cg_step_begin(const CgStepArgs& a, hipStream_t stream);
+hipError_t cg_step_prepare(const CgStepArgs& a, hipStream_t stream);
 hipError_t cg_step_end(const CgStepArgs& a, hipStream_t stream);
 bool skinny_gemm_supported(int64_t M, int64_t N, int64_t K);
 bool skinny_gemm_norm_supported(int64_t M, int64_t K);

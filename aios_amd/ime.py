@@ -784,8 +784,15 @@ class _DecodeGraph:
             self.ban_max = torch.zeros(1, dtype=torch.long, device=dev)  # longest ban
         self.tok = torch.zeros(rows, dtype=torch.long, device=dev)
         self.raw = torch.zeros(rows, dtype=torch.float32, device=dev)
+        self.step_next = torch.zeros(1, dtype=torch.long, device=dev)  # step + 1, per replay
         self.md = rt.model.attn_backend.prepare_static_decode(self.row_ids, kv_cap, plan_prefix,
                                                               rt.page_table)
+        # The step's preparation also gathers the embedding rows for a model
+        # that takes them (the standard trunk; the Block-AttnRes trunk
+        # gathers into its depth bank itself).
+        emb = rt.model.w["embed"]
+        self.h_in = (torch.empty((rows, emb.shape[1]), dtype=emb.dtype, device=dev)
+                     if getattr(rt.model, "takes_input_embeds", False) else None)
         reqs = [Req(input_ids=torch.empty(1), cached_len=0, output_len=1, uid=r,
                     sampling_params=SamplingParams(max_tokens=1), table_idx=r)
                 for r in range(rows)]
@@ -794,6 +801,7 @@ class _DecodeGraph:
         # page-table column the step attends to last
         self.batch.fused_append = True
         self.batch.input_ids = self.tokens
+        self.batch.input_embeds = self.h_in
         self.batch.positions = self.pos
         self.batch.attn_metadata = self.md
         self.graph: torch.cuda.CUDAGraph | None = None
@@ -815,7 +823,7 @@ class _DecodeGraph:
         prefix of that length, from the minimum prefix on; the pad id (or
         -1, none) elsewhere while a ban is that long (ime.py:977-996), -1
         outside that window."""
-        s = self.step + 1
+        s = self.step_next
         eq = (self.out_ids[:, None, :] == self.ban_ids[None, :, :]) | \
             (self.ban_cols >= s)[None, None, :]
         window = (s >= self.ban_min) & (s < self.ban_max)
@@ -852,23 +860,29 @@ class _DecodeGraph:
         self.step.zero_()
 
     def _body(self) -> None:
-        """One step: the page-table column (aios_cg_step_begin), metadata
-        refresh, model, pick, then the state update (aios_cg_step_end) --
-        the ime.py:1010-1054 bookkeeping in two launches."""
+        """One step: the page-table column, decode metadata, step column and
+        embedding rows (aios_cg_step_prepare), model, pick, then the state
+        update (aios_cg_step_end) -- the ime.py:1010-1054 bookkeeping in two
+        launches."""
         rt = self.rt
         lib = _lib.lib()
         pt = rt.page_table
+        md = self.md
         stream = torch.cuda.current_stream(self.rt.device).cuda_stream
-        _lib.check(lib.aios_cg_step_begin(
+        emb = rt.model.w["embed"]
+        _lib.check(lib.aios_cg_step_prepare(
             self.step.data_ptr(), self.pages.data_ptr(), self.pages.shape[0], self.rows,
             self.out_loc.data_ptr(), pt.data_ptr(), pt.stride(0), pt.shape[1],
-            self.pos.data_ptr(), stream), "aios_cg_step_begin")
-        self.md.refresh(self.pos[:1] + 1)
+            self.pos.data_ptr(), md.cu_seqlens_k_gpu.data_ptr(), md.indices.data_ptr(),
+            md.max_kv_len, self.step_next.data_ptr(), self.tokens.data_ptr(),
+            emb.data_ptr() if self.h_in is not None else None, emb.shape[0], emb.shape[1],
+            self.h_in.data_ptr() if self.h_in is not None else None, stream),
+            "aios_cg_step_prepare")
         self.batch.out_loc = self.out_loc
         with rt.ctx.forward_batch(self.batch):
             logits = rt.model.forward()
         if self.sampling is not None:
-            tok, raw = sample_step(logits, self.sampling, self.uni, self.step + 1, self.blocked,
+            tok, raw = sample_step(logits, self.sampling, self.uni, self.step_next, self.blocked,
                                    self.min_new, forbidden_by_row=(self._banned_next() if self.bans
                                                                    else None),
                                    out=(self.tok, self.raw))

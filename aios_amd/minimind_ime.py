@@ -81,6 +81,9 @@ class MiniMindBlockAttnResForCausalLM(Qwen3ForCausalLM):
     ``mlp_res_query`` / ``mlp_res_norm``; the final mixer's are
     ``final_res_query`` / ``final_res_norm``."""
 
+    # the embedding rows go straight into the depth bank (forward below)
+    takes_input_embeds = False
+
     def __init__(self, config: ModelConfig, weights: dict, device,
                  attn_backend: BaseAttentionBackend | None = None,
                  max_positions: int | None = None, ops=None) -> None:

@@ -95,6 +95,9 @@ class Qwen3ForCausalLM:
     add_rmsnorm_linear and qk_norm_rope (default: the gfx950 kernels,
     aios_amd.layers.HipOps)."""
 
+    # forward() uses batch.input_embeds when the caller gathered them
+    takes_input_embeds = True
+
     def __init__(self, config: ModelConfig, weights: dict, device,
                  attn_backend: BaseAttentionBackend | None = None,
                  max_positions: int | None = None, ops=None) -> None:
@@ -147,7 +150,8 @@ class Qwen3ForCausalLM:
         batch = ctx.batch
         c = self.config
         ops = self.ops
-        h = F.embedding(batch.input_ids, self.w["embed"])
+        h = (batch.input_embeds if batch.input_embeds is not None
+             else F.embedding(batch.input_ids, self.w["embed"]))
         positions = batch.positions
         residual = None
         for i, lw in enumerate(self.w["layers"]):

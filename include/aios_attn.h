@@ -374,6 +374,29 @@ int aios_cg_step_end(int64_t* step, int32_t rows, const int64_t* tok, const floa
                      int32_t* pos, int64_t* fed, void* stream);
 
 /*
+ * aios_cg_step_begin and the rest of what a captured decode step reads
+ * before the model, in one launch (the ime.py:1219-1251 page column, the
+ * decode metadata of flashinfer.py:209-250 for a group whose rows share
+ * their length, the sampler's step column and the embedding lookup of
+ * embedding.py:13-41):
+ *   the page-table column and out_loc as aios_cg_step_begin;
+ *   L = pos[0] + 1 clamped to [0, max_kv_len]; cu_k[b] = b * L for
+ *     b in [0, rows]; indices[b * L + j] = page_table[b][j] for j < L (the
+ *     column written this step read as out_loc[b]); rows are page-table
+ *     rows 0 .. rows-1;
+ *   *step_next = *step + 1 (step_next may be null);
+ *   embed non-null: h_out[r][:] = embed[tokens[r]][:] (bf16 [vocab][hidden],
+ *     hidden a multiple of 8, 16-byte aligned; ids clamped to [0, vocab)).
+ * cu_k holds rows + 1 and indices rows * max_kv_len entries; max_kv_len is
+ * at most pt_cols.
+ */
+int aios_cg_step_prepare(int64_t* step, const int32_t* pages, int32_t page_rows, int32_t rows,
+                         int32_t* out_loc, int32_t* page_table, int64_t pt_stride, int32_t pt_cols,
+                         int32_t* pos, int32_t* cu_k, int32_t* indices, int32_t max_kv_len,
+                         int64_t* step_next, const int64_t* tokens, const void* embed,
+                         int64_t vocab, int32_t hidden, void* h_out, void* stream);
+
+/*
  * Greedy selection over rows of logits (elem_bytes 2: bf16, 4: fp32):
  *   token_out[r]   = first index of the maximum of logits[r, 0 .. vocab)
  *   logprob_out[r] = logits[r, token] - logsumexp(logits[r, :])  (fp32)

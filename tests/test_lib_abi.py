@@ -145,3 +145,25 @@ def test_pool_of_2_24_pages_is_rejected():
                                   0.125, None)
         assert rc == _lib.AIOS_ERR_UNSUPPORTED
         assert what in lib.aios_last_error()
+
+
+def test_cg_step_prepare_rejects_bad_arguments():
+    """Argument checks run before any device access (fake pointers)."""
+    lib = _lib.lib()
+    P = 4096  # a 16-byte-aligned stand-in address, never dereferenced
+    args = lambda **kw: [kw.get("step", P), P, 4, 8, P, P, kw.get("pt_stride", 256),
+                         kw.get("pt_cols", 256), P, P, P, kw.get("max_kv_len", 128), None, P,
+                         kw.get("embed", None), kw.get("vocab", 100), kw.get("hidden", 768),
+                         kw.get("h_out", P), None]
+    rc = lib.aios_cg_step_prepare(*args(max_kv_len=300))
+    assert rc == _lib.AIOS_ERR_INVALID and b"max_kv_len" in lib.aios_last_error()
+    rc = lib.aios_cg_step_prepare(*args(pt_stride=100))
+    assert rc == _lib.AIOS_ERR_INVALID
+    rc = lib.aios_cg_step_prepare(*args(step=None))
+    assert rc == _lib.AIOS_ERR_INVALID and b"null pointer" in lib.aios_last_error()
+    rc = lib.aios_cg_step_prepare(*args(embed=P, hidden=100))
+    assert rc == _lib.AIOS_ERR_INVALID and b"multiple of 8" in lib.aios_last_error()
+    rc = lib.aios_cg_step_prepare(*args(embed=P + 8))
+    assert rc == _lib.AIOS_ERR_INVALID and b"16-byte" in lib.aios_last_error()
+    rc = lib.aios_cg_step_prepare(*args(embed=P, h_out=None))
+    assert rc == _lib.AIOS_ERR_INVALID
