@@ -240,6 +240,148 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
   }
 }
 
+// Projections with many 16-column tiles and up to 16 rows (the LM head: 9,496
+// tiles at a 151,936-id vocabulary), K = 128 * KS: a grid of a few
+// workgroups per compute unit, each walking tiles blockIdx.x, + gridDim.x,
+// ...  Its rows (normalised once with kAddNorm) stay in registers, and the W
+// fragments of the next tile are loaded while the current tile is
+// multiplied and reduced, so a workgroup pays the weight-load latency once
+// instead of once per tile (and the row norm once instead of per tile).
+// The loop issues loads only: the next tile's loads are unconditional (the
+// index clamped to the last tile) and the tiles' outputs are staged in LDS
+// and stored after the loop, so the compiler's load-counter waits let the
+// next tile's loads stay in flight.
+constexpr int kStreamWgsPerCu = 2;
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer descriptor word 3 (32-bit data format)
+constexpr int kStreamMaxIters = 32;  // tiles one workgroup stages in LDS
+
+template <int PRO, int KS>
+__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_stream_kernel(LinearArgs a) {
+  __shared__ f32x4 red[2][4][64];  // per tile parity: the four wavefronts' partials
+  __shared__ float ssq[4][16];
+  __shared__ uint2 out_s[kStreamMaxIters][64];  // a tile: 16 rows x 4 groups of 4 columns
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int l16 = lane & 15;
+  const int lg = lane >> 4;
+  const int k_begin = wave * (KS * 32) + lg * 8;  // K / 4 = KS * 32
+  const bool xok = l16 < a.M;
+  const int64_t m = xok ? l16 : 0;
+  const int64_t tiles = a.N / 16;
+  const int64_t G = gridDim.x;
+  // W through a raw buffer: the lane's offset is loop-invariant and a tile
+  // moves only the scalar offset, so the loop needs no vector registers for
+  // addresses (W below 2 GiB, checked by the launcher).
+  const __amdgpu_buffer_rsrc_t wrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, 0x7fffffff, kRsrcWord3);
+  const int32_t lane_off = (int32_t)((l16 * a.w_stride + k_begin) * 2);
+  const int64_t tile_bytes = 16 * a.w_stride * 2;
+  auto load_w = [&](bf16x8 (&w)[KS], int64_t tile) {
+    const int32_t soff = (int32_t)(min(tile, tiles - 1) * tile_bytes);
+#pragma unroll
+    for (int u = 0; u < KS; ++u)
+      w[u] = __builtin_bit_cast(bf16x8,
+                                __builtin_amdgcn_raw_buffer_load_b128(wrs, lane_off + u * 64, soff, 0));
+  };
+  int64_t t = blockIdx.x;  // < tiles: the grid is at most the tile count
+  bf16x8 wa[KS], wb[KS];
+  load_w(wa, t);
+
+  bf16x8 xb[KS];
+  if constexpr (PRO == kAddNorm) {
+    bf16x8 hf[KS], rf[KS], nw[KS];
+#pragma unroll
+    for (int u = 0; u < KS; ++u) {
+      nw[u] = *reinterpret_cast<const bf16x8*>(a.norm_w + k_begin + u * 32);
+      hf[u] = xok ? *reinterpret_cast<const bf16x8*>(a.x + m * a.x_stride + k_begin + u * 32)
+                  : bf16x8{};
+      rf[u] = (xok && a.residual)
+                  ? *reinterpret_cast<const bf16x8*>(a.residual + m * a.r_stride + k_begin + u * 32)
+                  : bf16x8{};
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < KS; ++u) {
+      float h8[8], r8[8];
+      unpack8(hf[u], h8);
+      unpack8(rf[u], r8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float r = h8[j] + r8[j];
+        ss = fmaf(r, r, ss);
+      }
+      if (a.residual_out && blockIdx.x == 0 && xok) {
+        float s8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s8[j] = h8[j] + r8[j];
+        *reinterpret_cast<bf16x8*>(a.residual_out + m * a.ro_stride + k_begin + u * 32) =
+            pack8(s8);
+      }
+    }
+    ss = xrow_sum(ss);
+    if (lg == 0) ssq[wave][l16] = ss;
+    __syncthreads();
+    const float inv =
+        rsqrtf((ssq[0][l16] + ssq[1][l16] + ssq[2][l16] + ssq[3][l16]) / (float)a.K + a.eps);
+#pragma unroll
+    for (int u = 0; u < KS; ++u) {
+      float w8[8], h8[8], r8[8], x8[8];
+      unpack8(nw[u], w8);
+      unpack8(hf[u], h8);
+      unpack8(rf[u], r8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x8[j] = (h8[j] + r8[j]) * inv * w8[j];
+      xb[u] = xok ? pack8(x8) : bf16x8{};
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < KS; ++u)
+      xb[u] = xok ? *reinterpret_cast<const bf16x8*>(a.x + m * a.x_stride + k_begin + u * 32)
+                  : bf16x8{};
+  }
+
+  // One tile: this wavefront's K-quarter product, the four partials summed
+  // through LDS by lanes lg == wave of every wavefront (row l16, columns
+  // 4 * wave ..), the result staged in out_s[it].
+  auto tile = [&](const bf16x8 (&w)[KS], int it, int par) {
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < KS; ++u) acc = mfma16x16x32(w[u], xb[u], acc);
+    red[par][wave][lane] = acc;
+    __syncthreads();
+    const int src = l16 + 16 * wave;
+    const f32x4 o = red[par][0][src] + red[par][1][src] + red[par][2][src] + red[par][3][src];
+    if (lg == wave) out_s[it][l16 * 4 + wave] = make_uint2(pack_bf16x2(o[0], o[1]),
+                                                           pack_bf16x2(o[2], o[3]));
+  };
+  // Every load so far (the first tile's, then the rows') has landed before
+  // the loop: with loads of unknown count pending where the loop header
+  // merges, the compiler would wait for all of them (vmcnt(0)) at the top of
+  // every iteration, before the next tile's loads go out.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  int it = 0;
+  while (true) {
+    load_w(wb, t + G);
+    tile(wa, it++, 0);
+    t += G;
+    if (t >= tiles) break;
+    load_w(wa, t + G);
+    tile(wb, it++, 1);
+    t += G;
+    if (t >= tiles) break;
+  }
+  __syncthreads();
+  // Tile i's rows: y[r][(blockIdx.x + i * G) * 16 + 4 * g ..] = out_s[i][r * 4 + g].
+  for (int c = threadIdx.x; c < it * 64; c += kGemmThreads) {
+    const int i = c >> 6;
+    const int r = (c >> 2) & 15;
+    const int g = c & 3;
+    if (r < a.M)
+      *reinterpret_cast<uint2*>(a.y + (int64_t)r * a.y_stride +
+                                ((int64_t)blockIdx.x + (int64_t)i * G) * 16 + 4 * g) = out_s[i][c & 63];
+  }
+}
+
 // Plain projections with K = 768 and up to 16 rows (the o projection and
 // LM head of hidden-768 models): one wavefront per 16 output columns over the
 // whole K, every load in one round trip, two interleaved MFMA chains, no LDS
@@ -313,7 +455,43 @@ bool skinny_gemm_norm_supported(int64_t M, int64_t K) {
   return mt >= 1 && mt <= 4 && (K / 4) / 32 <= kNormMaxFrags / mt;
 }
 
+// Compute units of the current device (looked up once per process).
+int stream_grid_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    cus = (hipGetDevice(&dev) == hipSuccess &&
+           hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+           n > 0)
+              ? n
+              : 256;
+  }
+  return cus;
+}
+
+template <int PRO, int KS>
+hipError_t launch_stream(const LinearArgs& a, int64_t grid, hipStream_t stream) {
+  hipLaunchKernelGGL((skinny_gemm_stream_kernel<PRO, KS>), dim3((unsigned)grid),
+                     dim3(kGemmThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
 hipError_t skinny_gemm(const LinearArgs& a, int prologue, int epilogue, hipStream_t stream) {
+  // Many column tiles, one row tile, K 768 / 1024: the streaming kernel,
+  // when every workgroup then walks at least two tiles (and at most the
+  // tiles it can stage).
+  const int64_t stream_grid = (int64_t)kStreamWgsPerCu * stream_grid_cus();
+  const int64_t tiles = a.N / 16;
+  if (epilogue == kStore && a.M <= 16 && tiles >= 2 * stream_grid &&
+      tiles <= (int64_t)kStreamMaxIters * stream_grid && (a.K == 768 || a.K == 1024) &&
+      a.N * a.w_stride * 2 < ((int64_t)1 << 31)) {
+    if (prologue == kPlain)
+      return a.K == 768 ? launch_stream<kPlain, 6>(a, stream_grid, stream)
+                        : launch_stream<kPlain, 8>(a, stream_grid, stream);
+    if (prologue == kAddNorm)
+      return a.K == 768 ? launch_stream<kAddNorm, 6>(a, stream_grid, stream)
+                        : launch_stream<kAddNorm, 8>(a, stream_grid, stream);
+  }
   if (prologue == kPlain && epilogue == kStore && a.M <= 16 && a.K == kColsSteps * 32) {
     hipLaunchKernelGGL(skinny_gemm_cols_kernel, dim3((unsigned)(a.N / 16)), dim3(64), 0, stream, a);
     return hipGetLastError();

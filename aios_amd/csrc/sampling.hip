@@ -18,7 +18,9 @@
 namespace aios {
 namespace {
 
-constexpr int kGreedyThreads = 1024;  // a 151,936-id bf16 row in ~2.4 round trips of one workgroup
+constexpr int kGreedyThreads = 1024;  // rows above kGreedyWideFrom ids: 151,936 in ~2.4 round trips
+constexpr int kGreedyThreadsNarrow = 256;  // shorter rows: one round trip, fewer wavefronts to merge
+constexpr int kGreedyWideFrom = 32768;
 
 struct ArgState {
   float m;    // running maximum (log2-scaled)
@@ -60,8 +62,8 @@ __device__ __forceinline__ void load8f(const float* p, float* f) {
 
 constexpr int kGreedyUnroll = 8;  // 8-logit chunks per thread in flight (128 KiB per workgroup)
 
-template <typename T>
-__global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
+template <typename T, int NT>
+__global__ __launch_bounds__(NT) void greedy_kernel(
     const T* __restrict__ logits, int64_t row_stride, int32_t vocab,
     int64_t* __restrict__ token_out, float* __restrict__ logprob_out) {
   const int row = blockIdx.x;
@@ -82,12 +84,12 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
   // is skipped), then the rest one by one.  Each thread visits its ids in
   // increasing order, so its state keeps the first index of its maximum.
   const int whole = ((uintptr_t)x & 15) == 0 ? (vocab & ~7) : 0;
-  for (int base = 0; base < whole; base += kGreedyThreads * 8 * kGreedyUnroll) {
+  for (int base = 0; base < whole; base += NT * 8 * kGreedyUnroll) {
     float f[kGreedyUnroll][8];
     int i0[kGreedyUnroll];
 #pragma unroll
     for (int u = 0; u < kGreedyUnroll; ++u) {
-      i0[u] = base + (u * kGreedyThreads + (int)threadIdx.x) * 8;
+      i0[u] = base + (u * NT + (int)threadIdx.x) * 8;
       load8f(x + min(i0[u], whole - 8), f[u]);
     }
 #pragma unroll
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
         for (int j = 0; j < 8; ++j) visit(f[u][j], i0[u] + j);
       }
   }
-  for (int32_t j = whole + threadIdx.x; j < vocab; j += kGreedyThreads) visit(load_logit(x + j), j);
+  for (int32_t j = whole + threadIdx.x; j < vocab; j += NT) visit(load_logit(x + j), j);
   for (int off = 32; off > 0; off >>= 1) {
     ArgState o;
     o.m = __shfl_xor(st.m, off);
@@ -105,14 +107,14 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(
     o.s = __shfl_xor(st.s, off);
     st = merge(st, o);
   }
-  __shared__ ArgState waves[kGreedyThreads / 64];
+  __shared__ ArgState waves[NT / 64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   if (lane == 0) waves[wave] = st;
   __syncthreads();
   if (threadIdx.x == 0) {
     ArgState r = waves[0];
-    for (int w = 1; w < kGreedyThreads / 64; ++w) r = merge(r, waves[w]);
+    for (int w = 1; w < NT / 64; ++w) r = merge(r, waves[w]);
     token_out[row] = r.i;
     // log_softmax at the maximum: -ln(sum exp(x - max)).
     logprob_out[row] = -fast_log2(r.s) * 0.6931471805599453f;
@@ -1380,14 +1382,25 @@ hipError_t greedy_select(const void* logits, int64_t row_stride, int32_t rows, i
                          int32_t elem_bytes, int64_t* token_out, float* logprob_out,
                          hipStream_t stream) {
   if (rows == 0) return hipSuccess;
+  const bool wide = vocab > kGreedyWideFrom;
   if (elem_bytes == 2) {
-    hipLaunchKernelGGL(greedy_kernel<bf16>, dim3(rows), dim3(kGreedyThreads), 0, stream,
-                       static_cast<const bf16*>(logits), row_stride, vocab, token_out,
-                       logprob_out);
+    const bf16* x = static_cast<const bf16*>(logits);
+    if (wide)
+      hipLaunchKernelGGL((greedy_kernel<bf16, kGreedyThreads>), dim3(rows), dim3(kGreedyThreads),
+                         0, stream, x, row_stride, vocab, token_out, logprob_out);
+    else
+      hipLaunchKernelGGL((greedy_kernel<bf16, kGreedyThreadsNarrow>), dim3(rows),
+                         dim3(kGreedyThreadsNarrow), 0, stream, x, row_stride, vocab, token_out,
+                         logprob_out);
   } else {
-    hipLaunchKernelGGL(greedy_kernel<float>, dim3(rows), dim3(kGreedyThreads), 0, stream,
-                       static_cast<const float*>(logits), row_stride, vocab, token_out,
-                       logprob_out);
+    const float* x = static_cast<const float*>(logits);
+    if (wide)
+      hipLaunchKernelGGL((greedy_kernel<float, kGreedyThreads>), dim3(rows), dim3(kGreedyThreads),
+                         0, stream, x, row_stride, vocab, token_out, logprob_out);
+    else
+      hipLaunchKernelGGL((greedy_kernel<float, kGreedyThreadsNarrow>), dim3(rows),
+                         dim3(kGreedyThreadsNarrow), 0, stream, x, row_stride, vocab, token_out,
+                         logprob_out);
   }
   return hipGetLastError();
 }

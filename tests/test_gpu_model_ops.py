@@ -73,7 +73,11 @@ def test_silu_and_mul(rows, inter):
 
 @pytest.mark.parametrize("m,n,k", [(1, 1152, 768), (8, 1152, 768), (8, 768, 768), (8, 4096, 768),
                                    (8, 768, 2048), (8, 6400, 768), (24, 1024, 4096),
-                                   (17, 2048, 1024), (64, 256, 9728), (33, 16, 128)])
+                                   (17, 2048, 1024), (64, 256, 9728), (33, 16, 128),
+                                   # many column tiles: the streaming kernel (even and
+                                   # uneven tiles per workgroup)
+                                   (8, 16384, 768), (5, 20016, 768), (16, 32768, 1024),
+                                   (8, 151936, 1024)])
 def test_linear_rows_matches_fp32_gemm(m, n, k):
     """Few-row GEMM kernel vs an fp32 matmul of the same bf16 operands: fp32
     accumulation, one bf16 rounding at the end."""
@@ -98,7 +102,10 @@ def test_linear_rows_strided_input_and_fallback():
 
 @pytest.mark.parametrize("rows,k,n", [(1, 768, 1152), (8, 768, 1152), (8, 768, 6400),
                                       (24, 1024, 512), (40, 512, 256), (8, 2048, 768),
-                                      (24, 768, 1152), (17, 768, 1152)])
+                                      (24, 768, 1152), (17, 768, 1152),
+                                      # the streaming kernel (LM-head shapes)
+                                      (8, 768, 16384), (1, 768, 20016), (8, 1024, 151936),
+                                      (24, 1024, 151936)])
 @pytest.mark.parametrize("with_residual", [True, False])
 def test_add_rmsnorm_linear(rows, k, n, with_residual):
     """RMSNorm (with the residual add) folded into the projection: the same
