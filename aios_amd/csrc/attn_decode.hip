@@ -192,7 +192,6 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
     return lane < T::CPR ? __builtin_bit_cast(uint4, qk_rope8(x, p, c < HALF, k_c, k_s))
                          : make_uint4(0u, 0u, 0u, 0u);
   };
-  uint4 knew = make_uint4(0u, 0u, 0u, 0u);
   bool rope_pending = rope;
   const uint32_t tok_b = (uint32_t)(a.kv_tok_stride * 2);
   const uint32_t n_pages = (uint32_t)a.num_pages;
@@ -235,6 +234,12 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
       __builtin_amdgcn_global_load_lds(src, (AIOS_LDS void*)(buf + j * 64 * 16), 16, 0, 0);
     }
     if (rope_pending) {
+      // The rotation inputs go out right behind the sub-tile's loads and
+      // are waited for with them: the scheduling barriers keep the
+      // compiler from hoisting them above the page-id loads (the in-order
+      // load counter would then hold the page ids behind the table loads)
+      // or sinking them below the wait (a second round trip).
+      __builtin_amdgcn_sched_barrier(0);
       const bf16* cr = a.rope_cos + rrow * D;
       const bf16* sr = a.rope_sin + rrow * D;
       eng.rope_load(qin, qrow, l16 < G, a.q_norm);
@@ -245,15 +250,31 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
         k_c = *reinterpret_cast<const bf16x8*>(cr + lane * 8);
         k_s = *reinterpret_cast<const bf16x8*>(sr + lane * 8);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
     wait_vmcnt<0>();
+    // The rotated new K row lives only in this iteration (kept across the
+    // loop it was spilled to scratch, a memory round trip before its LDS
+    // write and another before the cache store): it goes to its cache page
+    // as soon as it is computed, and into this sub-tile if the new token
+    // is in it; a later sub-tile of this wavefront reads it back from the
+    // page (this wavefront's own store, complete after wait_vmcnt<0>; no
+    // other workgroup touches that page, so no cache holds an older copy).
+    uint4 knew = make_uint4(0u, 0u, 0u, 0u);
+    bool knew_here = false;
     if (rope_pending) {
       eng.rope_finish(0, qin, l16 < G, a.norm_eps);
-      if (new_here) knew = k_rope();
+      if (new_here) {
+        knew = k_rope();
+        knew_here = true;
+        if (new_ok && lane < T::CPR)
+          *reinterpret_cast<uint4*>(const_cast<uint8_t*>(kc) + new_dst * tok_b + lane * 16) = knew;
+      }
       rope_pending = false;
     }
     if (rope && new_ok && kv0 <= t_new && t_new < kv0 + kSubTok && lane < T::CPR) {
       const int tl = t_new - kv0;
+      if (!knew_here) knew = *reinterpret_cast<const uint4*>(kc + new_dst * tok_b + lane * 16);
       *reinterpret_cast<uint4*>(buf + tl * T::ROWB + T::k_slot(tl, lane) * 16) = knew;
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -261,10 +282,11 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   }
   eng.finish();
 
-  if (new_ok && new_here && lane < 2 * T::CPR) {
+  // The new token's rows to its page (with the rotation, K went already).
+  if (new_ok && new_here && lane < 2 * T::CPR && !(rope && lane < T::CPR)) {
     const bool isv = lane >= T::CPR;
     const int c = isv ? lane - T::CPR : lane;
-    const uint4 v = (rope && !isv) ? knew : *reinterpret_cast<const uint4*>((isv ? vn : kn) + c * 16);
+    const uint4 v = *reinterpret_cast<const uint4*>((isv ? vn : kn) + c * 16);
     *reinterpret_cast<uint4*>(const_cast<uint8_t*>(isv ? vc : kc) + new_dst * tok_b + c * 16) = v;
   }
 
