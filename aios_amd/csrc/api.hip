@@ -31,7 +31,7 @@ int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 int32_t cdiv(int32_t a, int32_t b) { return (a + b - 1) / b; }
 
 // Shared prefixes shorter than this are read per row (no second launch).
-constexpr int32_t kMinCascadePrefix = 128;
+constexpr int32_t kMinCascadePrefix = 256;
 // Partial states per (row, kv-head) the combine merges (one per lane of a
 // wavefront when it computes the merge weights).
 constexpr int32_t kMaxParts = 64;

@@ -197,10 +197,10 @@ def test_candidate_group_minimind_0p1b():
 
 
 def test_candidate_group_long_prefix_cascade():
-    """Prefix >= 128 tokens: the decode plan uses the shared-prefix cascade."""
+    """Prefix >= 256 tokens: the decode plan uses the shared-prefix cascade."""
     c = replace(QWEN3_0P6B, num_layers=3, vocab_size=8192)
     eng, om = _engine(c, 11)
-    prefix = _prefix(11, 200, c.vocab_size)
+    prefix = _prefix(11, 300, c.vocab_size)
     plans = []
     inner = eng.rt.model.attn_backend.prepare_metadata
 
@@ -212,7 +212,7 @@ def test_candidate_group_long_prefix_cascade():
     eng.rt.model.attn_backend.prepare_metadata = spy
     _check_candidate_group(eng, om, prefix, 8, 6)
     decode_plans = [p for p in plans if p[0] == "decode"]
-    assert decode_plans and all(p[2] == 200 and p[1] >= 1 for p in decode_plans)
+    assert decode_plans and all(p[2] == 300 and p[1] >= 1 for p in decode_plans)
 
 
 def test_lcp_extension_and_strict_backspace():
