@@ -797,7 +797,7 @@ class _DecodeGraph:
                     sampling_params=SamplingParams(max_tokens=1), table_idx=r)
                 for r in range(rows)]
         self.batch = Batch(reqs=reqs, phase="decode")
-        # aios_cg_step_begin writes each row's page into both out_loc and the
+        # aios_cg_step_prepare writes each row's page into both out_loc and the
         # page-table column the step attends to last
         self.batch.fused_append = True
         self.batch.input_ids = self.tokens
