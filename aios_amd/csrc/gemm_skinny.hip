@@ -49,8 +49,12 @@ __device__ __forceinline__ bf16x8 pack8(const float* f) {
 
 // KS > 0: the K steps of a wavefront (K / 128) fixed at compile time, so
 // the operand loads are one straight-line burst; KS = 0: read from K.
-template <int MT, int PRO, int EPI, int KS = 0>
+// NC = 8: a workgroup owns 8 output columns (W rows 8..15 of the MFMA tile
+// are not loaded and read as zero), twice the workgroups at half the weight
+// bytes each, for projections with few column tiles.
+template <int MT, int PRO, int EPI, int KS = 0, int NC = 16>
 __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a) {
+  static_assert(NC == 16 || (NC == 8 && PRO == kPlain && EPI == kStore), "8-column tiles: plain");
   constexpr int NP = EPI == kSiluPair ? 2 : 1;  // W row sets per workgroup
   __shared__ f32x4 red[3][NP][MT][64];
   __shared__ float ssq[4][MT][16];
@@ -58,12 +62,13 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
   const int wave = threadIdx.x >> 6;
   const int l16 = lane & 15;
   const int lg = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t n0 = (int64_t)blockIdx.x * NC;
   const int kq = a.K >> 2;  // multiple of 32
   const int k_begin = wave * kq + lg * 8;
   const int steps = KS > 0 ? KS : kq >> 5;
+  const bool wok = NC == 16 || l16 < NC;  // this lane's W row is one of the tile's
   const bf16* wrow[NP];
-  wrow[0] = a.w + (n0 + l16) * a.w_stride + k_begin;
+  wrow[0] = a.w + (n0 + (wok ? l16 : 0)) * a.w_stride + k_begin;
   if constexpr (NP == 2) wrow[NP - 1] = a.w + (a.N + n0 + l16) * a.w_stride + k_begin;
   int64_t xoff[MT], roff[MT];
   bool xok[MT];
@@ -188,7 +193,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
         if (s0 + u < steps) {
 #pragma unroll
           for (int p = 0; p < NP; ++p)
-            wa[p][u] = *reinterpret_cast<const bf16x8*>(wrow[p] + (s0 + u) * 32);
+            wa[p][u] = wok ? *reinterpret_cast<const bf16x8*>(wrow[p] + (s0 + u) * 32) : bf16x8{};
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
             b[u][mt] = xok[mt] ? *reinterpret_cast<const bf16x8*>(a.x + xoff[mt] + (s0 + u) * 32)
@@ -233,6 +238,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
         o[i] = round_bf16(g / (1.f + expf(-g))) * u;
       }
     }
+    if (NC == 8 && lg >= 2) continue;  // columns 8..15 of the MFMA tile: not this tile's
     uint2 packed;
     packed.x = pack_bf16x2(o[0], o[1]);
     packed.y = pack_bf16x2(o[2], o[3]);
@@ -425,7 +431,12 @@ hipError_t launch_pe(const LinearArgs& a, hipStream_t stream) {
       case 6: hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 6>), grid, dim3(kGemmThreads), 0, stream, a); return hipGetLastError();
       case 8: hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 8>), grid, dim3(kGemmThreads), 0, stream, a); return hipGetLastError();
       case 16:
-        if constexpr (PRO == kPlain) {
+        if constexpr (PRO == kPlain && EPI == kStore) {
+          // the down projection (K 2048, N = hidden): 8-column tiles
+          hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 16, 8>), dim3((unsigned)(a.N / 8)),
+                             dim3(kGemmThreads), 0, stream, a);
+          return hipGetLastError();
+        } else if constexpr (PRO == kPlain) {
           hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 16>), grid, dim3(kGemmThreads), 0, stream, a);
           return hipGetLastError();
         }

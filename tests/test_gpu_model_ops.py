@@ -77,7 +77,9 @@ def test_silu_and_mul(rows, inter):
                                    # many column tiles: the streaming kernel (even and
                                    # uneven tiles per workgroup)
                                    (8, 16384, 768), (5, 20016, 768), (16, 32768, 1024),
-                                   (8, 151936, 1024)])
+                                   (8, 151936, 1024),
+                                   # K 2048 plain (the down projection): 8-column tiles
+                                   (1, 16, 2048), (16, 1024, 2048)])
 def test_linear_rows_matches_fp32_gemm(m, n, k):
     """Few-row GEMM kernel vs an fp32 matmul of the same bf16 operands: fp32
     accumulation, one bf16 rounding at the end."""
