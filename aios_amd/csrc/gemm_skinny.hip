@@ -54,7 +54,7 @@ __device__ __forceinline__ bf16x8 pack8(const float* f) {
 // bytes each, for projections with few column tiles.
 template <int MT, int PRO, int EPI, int KS = 0, int NC = 16>
 __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a) {
-  static_assert(NC == 16 || (NC == 8 && PRO == kPlain && EPI == kStore), "8-column tiles: plain");
+  static_assert(NC == 16 || (NC == 8 && MT == 1), "8-column tiles: one row tile");
   constexpr int NP = EPI == kSiluPair ? 2 : 1;  // W row sets per workgroup
   __shared__ f32x4 red[3][NP][MT][64];
   __shared__ float ssq[4][MT][16];
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
   const bool wok = NC == 16 || l16 < NC;  // this lane's W row is one of the tile's
   const bf16* wrow[NP];
   wrow[0] = a.w + (n0 + (wok ? l16 : 0)) * a.w_stride + k_begin;
-  if constexpr (NP == 2) wrow[NP - 1] = a.w + (a.N + n0 + l16) * a.w_stride + k_begin;
+  if constexpr (NP == 2) wrow[NP - 1] = a.w + (a.N + n0 + (wok ? l16 : 0)) * a.w_stride + k_begin;
   int64_t xoff[MT], roff[MT];
   bool xok[MT];
 #pragma unroll
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
     for (int p = 0; p < NP; ++p)
 #pragma unroll
       for (int u = 0; u < kGemmBatch; ++u)
-        if (u < steps) wa[p][u] = *reinterpret_cast<const bf16x8*>(wrow[p] + u * 32);
+        if (u < steps) wa[p][u] = wok ? *reinterpret_cast<const bf16x8*>(wrow[p] + u * 32) : bf16x8{};
     float ss[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) ss[mt] = 0.f;
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
 #pragma unroll
           for (int u = 0; u < kGemmBatch; ++u)
             if (s0 + u < steps)
-              wa[p][u] = *reinterpret_cast<const bf16x8*>(wrow[p] + (s0 + u) * 32);
+              wa[p][u] = wok ? *reinterpret_cast<const bf16x8*>(wrow[p] + (s0 + u) * 32) : bf16x8{};
       }
 #pragma unroll
       for (int u = 0; u < kGemmBatch; ++u) {
@@ -422,36 +422,46 @@ __global__ __launch_bounds__(64) void skinny_gemm_cols_kernel(LinearArgs a) {
   *reinterpret_cast<uint2*>(a.y + (int64_t)l16 * a.y_stride + n0 + lg * 4) = packed;
 }
 
+template <int MT, int PRO, int EPI, int KS, int NC>
+hipError_t launch_tiles(const LinearArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((skinny_gemm_kernel<MT, PRO, EPI, KS, NC>), dim3((unsigned)(a.N / NC)),
+                     dim3(kGemmThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+// narrow: 8-column tiles for one row tile (projections with at most one
+// 16-column tile per two compute units: twice the workgroups at half the
+// weight bytes each).  Measured per replayed decode step: the hidden-768
+// models' qkv, gate/up and down (80, 128, 48 tiles) gain ~2%; Qwen3-0.6B's
+// qkv and gate/up (256 and 192 tiles, each workgroup also re-reading its
+// 32 KB of norm-prologue rows) lost 5% with 8-column tiles.
 template <int PRO, int EPI>
-hipError_t launch_pe(const LinearArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)(a.N / 16));
+hipError_t launch_pe(const LinearArgs& a, bool narrow, hipStream_t stream) {
   if ((a.M + 15) / 16 == 1) {
-    // the decode-step shapes: K = 768, 1024, 2048 (one 16-row tile)
+    // the decode-step shapes: K = 768, 1024, 2048 with a fixed step count
     switch (a.K / 128) {
-      case 6: hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 6>), grid, dim3(kGemmThreads), 0, stream, a); return hipGetLastError();
-      case 8: hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 8>), grid, dim3(kGemmThreads), 0, stream, a); return hipGetLastError();
+      case 6:
+        return narrow ? launch_tiles<1, PRO, EPI, 6, 8>(a, stream)
+                      : launch_tiles<1, PRO, EPI, 6, 16>(a, stream);
+      case 8:
+        return narrow ? launch_tiles<1, PRO, EPI, 8, 8>(a, stream)
+                      : launch_tiles<1, PRO, EPI, 8, 16>(a, stream);
       case 16:
-        if constexpr (PRO == kPlain && EPI == kStore) {
-          // the down projection (K 2048, N = hidden): 8-column tiles
-          hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 16, 8>), dim3((unsigned)(a.N / 8)),
-                             dim3(kGemmThreads), 0, stream, a);
-          return hipGetLastError();
-        } else if constexpr (PRO == kPlain) {
-          hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI, 16>), grid, dim3(kGemmThreads), 0, stream, a);
-          return hipGetLastError();
-        }
+        if constexpr (PRO == kPlain)
+          return narrow ? launch_tiles<1, PRO, EPI, 16, 8>(a, stream)
+                        : launch_tiles<1, PRO, EPI, 16, 16>(a, stream);
         break;
       default: break;
     }
+    return narrow ? launch_tiles<1, PRO, EPI, 0, 8>(a, stream)
+                  : launch_tiles<1, PRO, EPI, 0, 16>(a, stream);
   }
   switch ((a.M + 15) / 16) {
-    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<1, PRO, EPI>), grid, dim3(kGemmThreads), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<2, PRO, EPI>), grid, dim3(kGemmThreads), 0, stream, a); break;
-    case 3: hipLaunchKernelGGL((skinny_gemm_kernel<3, PRO, EPI>), grid, dim3(kGemmThreads), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((skinny_gemm_kernel<4, PRO, EPI>), grid, dim3(kGemmThreads), 0, stream, a); break;
+    case 2: return launch_tiles<2, PRO, EPI, 0, 16>(a, stream);
+    case 3: return launch_tiles<3, PRO, EPI, 0, 16>(a, stream);
+    case 4: return launch_tiles<4, PRO, EPI, 0, 16>(a, stream);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace
@@ -507,11 +517,14 @@ hipError_t skinny_gemm(const LinearArgs& a, int prologue, int epilogue, hipStrea
     hipLaunchKernelGGL(skinny_gemm_cols_kernel, dim3((unsigned)(a.N / 16)), dim3(64), 0, stream, a);
     return hipGetLastError();
   }
-  if (prologue == kPlain && epilogue == kStore) return launch_pe<kPlain, kStore>(a, stream);
-  if (prologue == kPlain && epilogue == kSiluPair) return launch_pe<kPlain, kSiluPair>(a, stream);
-  if (prologue == kAddNorm && epilogue == kStore) return launch_pe<kAddNorm, kStore>(a, stream);
+  const bool narrow = 2 * tiles <= stream_grid_cus();
+  if (prologue == kPlain && epilogue == kStore) return launch_pe<kPlain, kStore>(a, narrow, stream);
+  if (prologue == kPlain && epilogue == kSiluPair)
+    return launch_pe<kPlain, kSiluPair>(a, narrow, stream);
+  if (prologue == kAddNorm && epilogue == kStore)
+    return launch_pe<kAddNorm, kStore>(a, narrow, stream);
   if (prologue == kAddNorm && epilogue == kSiluPair)
-    return launch_pe<kAddNorm, kSiluPair>(a, stream);
+    return launch_pe<kAddNorm, kSiluPair>(a, narrow, stream);
   return hipErrorInvalidValue;
 }
 
