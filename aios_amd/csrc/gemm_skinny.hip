@@ -49,12 +49,12 @@ __device__ __forceinline__ bf16x8 pack8(const float* f) {
 
 // KS > 0: the K steps of a wavefront (K / 128) fixed at compile time, so
 // the operand loads are one straight-line burst; KS = 0: read from K.
-// NC = 8: a workgroup owns 8 output columns (W rows 8..15 of the MFMA tile
-// are not loaded and read as zero), twice the workgroups at half the weight
-// bytes each, for projections with few column tiles.
+// NC = 8 / 4: a workgroup owns 8 / 4 output columns (the MFMA tile's other W
+// rows are not loaded and read as zero), 2x / 4x the workgroups at 1/2 / 1/4
+// of the weight bytes each, for projections with few column tiles.
 template <int MT, int PRO, int EPI, int KS = 0, int NC = 16>
 __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a) {
-  static_assert(NC == 16 || (NC == 8 && MT == 1), "8-column tiles: one row tile");
+  static_assert(NC == 16 || ((NC == 8 || NC == 4) && MT == 1), "narrow tiles: one row tile");
   constexpr int NP = EPI == kSiluPair ? 2 : 1;  // W row sets per workgroup
   __shared__ f32x4 red[3][NP][MT][64];
   __shared__ float ssq[4][MT][16];
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a)
         o[i] = round_bf16(g / (1.f + expf(-g))) * u;
       }
     }
-    if (NC == 8 && lg >= 2) continue;  // columns 8..15 of the MFMA tile: not this tile's
+    if (lg * 4 >= NC) continue;  // columns NC..15 of the MFMA tile: not this tile's
     uint2 packed;
     packed.x = pack_bf16x2(o[0], o[1]);
     packed.y = pack_bf16x2(o[2], o[3]);
@@ -429,32 +429,34 @@ hipError_t launch_tiles(const LinearArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// narrow: 8-column tiles for one row tile (projections with at most one
-// 16-column tile per two compute units: twice the workgroups at half the
-// weight bytes each).  Measured per replayed decode step: the hidden-768
+// nc: columns per workgroup for one row tile -- 8 for projections with at
+// most one 16-column tile per two compute units, 4 for at most one per
+// four (2x / 4x the workgroups at 1/2 / 1/4 of the weight bytes each; the
+// MFMA tile's other W rows read as zero).  Measured per replayed decode step: the hidden-768
 // models' qkv, gate/up and down (80, 128, 48 tiles) gain ~2%; Qwen3-0.6B's
 // qkv and gate/up (256 and 192 tiles, each workgroup also re-reading its
-// 32 KB of norm-prologue rows) lost 5% with 8-column tiles.
+// 32 KB of norm-prologue rows) lost 5% with 8-column tiles.  4 columns for
+// the down and o projections (48-64 tiles) gained another 1-2%.
+template <int PRO, int EPI, int KS>
+hipError_t launch_one_tile(const LinearArgs& a, int nc, hipStream_t stream) {
+  if (nc == 4) return launch_tiles<1, PRO, EPI, KS, 4>(a, stream);
+  if (nc == 8) return launch_tiles<1, PRO, EPI, KS, 8>(a, stream);
+  return launch_tiles<1, PRO, EPI, KS, 16>(a, stream);
+}
+
 template <int PRO, int EPI>
-hipError_t launch_pe(const LinearArgs& a, bool narrow, hipStream_t stream) {
+hipError_t launch_pe(const LinearArgs& a, int nc, hipStream_t stream) {
   if ((a.M + 15) / 16 == 1) {
     // the decode-step shapes: K = 768, 1024, 2048 with a fixed step count
     switch (a.K / 128) {
-      case 6:
-        return narrow ? launch_tiles<1, PRO, EPI, 6, 8>(a, stream)
-                      : launch_tiles<1, PRO, EPI, 6, 16>(a, stream);
-      case 8:
-        return narrow ? launch_tiles<1, PRO, EPI, 8, 8>(a, stream)
-                      : launch_tiles<1, PRO, EPI, 8, 16>(a, stream);
+      case 6: return launch_one_tile<PRO, EPI, 6>(a, nc, stream);
+      case 8: return launch_one_tile<PRO, EPI, 8>(a, nc, stream);
       case 16:
-        if constexpr (PRO == kPlain)
-          return narrow ? launch_tiles<1, PRO, EPI, 16, 8>(a, stream)
-                        : launch_tiles<1, PRO, EPI, 16, 16>(a, stream);
+        if constexpr (PRO == kPlain) return launch_one_tile<PRO, EPI, 16>(a, nc, stream);
         break;
       default: break;
     }
-    return narrow ? launch_tiles<1, PRO, EPI, 0, 8>(a, stream)
-                  : launch_tiles<1, PRO, EPI, 0, 16>(a, stream);
+    return launch_one_tile<PRO, EPI, 0>(a, nc, stream);
   }
   switch ((a.M + 15) / 16) {
     case 2: return launch_tiles<2, PRO, EPI, 0, 16>(a, stream);
@@ -517,14 +519,15 @@ hipError_t skinny_gemm(const LinearArgs& a, int prologue, int epilogue, hipStrea
     hipLaunchKernelGGL(skinny_gemm_cols_kernel, dim3((unsigned)(a.N / 16)), dim3(64), 0, stream, a);
     return hipGetLastError();
   }
-  const bool narrow = 2 * tiles <= stream_grid_cus();
-  if (prologue == kPlain && epilogue == kStore) return launch_pe<kPlain, kStore>(a, narrow, stream);
+  const int cus = stream_grid_cus();
+  const int nc = 4 * tiles <= cus ? 4 : (2 * tiles <= cus ? 8 : 16);
+  if (prologue == kPlain && epilogue == kStore) return launch_pe<kPlain, kStore>(a, nc, stream);
   if (prologue == kPlain && epilogue == kSiluPair)
-    return launch_pe<kPlain, kSiluPair>(a, narrow, stream);
+    return launch_pe<kPlain, kSiluPair>(a, nc, stream);
   if (prologue == kAddNorm && epilogue == kStore)
-    return launch_pe<kAddNorm, kStore>(a, narrow, stream);
+    return launch_pe<kAddNorm, kStore>(a, nc, stream);
   if (prologue == kAddNorm && epilogue == kSiluPair)
-    return launch_pe<kAddNorm, kSiluPair>(a, narrow, stream);
+    return launch_pe<kAddNorm, kSiluPair>(a, nc, stream);
   return hipErrorInvalidValue;
 }
 
