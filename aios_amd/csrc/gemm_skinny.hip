@@ -394,18 +394,22 @@ __global__ __launch_bounds__(kGemmThreads) void skinny_gemm_stream_kernel(Linear
 // reduction or barrier.
 constexpr int kColsSteps = 24;  // K = 768
 
+// NC columns per wavefront (16, or 8 / 4 with the MFMA tile's other W rows
+// read as zero, for projections with few column tiles).
+template <int NC>
 __global__ __launch_bounds__(64) void skinny_gemm_cols_kernel(LinearArgs a) {
   const int lane = threadIdx.x;
   const int l16 = lane & 15;
   const int lg = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const bf16* wr = a.w + (n0 + l16) * a.w_stride + lg * 8;
+  const int64_t n0 = (int64_t)blockIdx.x * NC;
+  const bool wok = l16 < NC;
+  const bf16* wr = a.w + (n0 + (wok ? l16 : 0)) * a.w_stride + lg * 8;
   const bool ok = l16 < a.M;
   const bf16* xr = a.x + (int64_t)(ok ? l16 : 0) * a.x_stride + lg * 8;
   bf16x8 w[kColsSteps], x[kColsSteps];
 #pragma unroll
   for (int s = 0; s < kColsSteps; ++s) {
-    w[s] = *reinterpret_cast<const bf16x8*>(wr + s * 32);
+    w[s] = wok ? *reinterpret_cast<const bf16x8*>(wr + s * 32) : bf16x8{};
     x[s] = *reinterpret_cast<const bf16x8*>(xr + s * 32);
   }
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
@@ -414,7 +418,7 @@ __global__ __launch_bounds__(64) void skinny_gemm_cols_kernel(LinearArgs a) {
     acc0 = mfma16x16x32(w[s], x[s], acc0);
     acc1 = mfma16x16x32(w[s + 1], x[s + 1], acc1);
   }
-  if (!ok) return;
+  if (!ok || lg * 4 >= NC) return;
   const f32x4 o = acc0 + acc1;
   uint2 packed;
   packed.x = pack_bf16x2(o[0], o[1]);
@@ -516,7 +520,13 @@ hipError_t skinny_gemm(const LinearArgs& a, int prologue, int epilogue, hipStrea
                         : launch_stream<kAddNorm, 8>(a, stream_grid, stream);
   }
   if (prologue == kPlain && epilogue == kStore && a.M <= 16 && a.K == kColsSteps * 32) {
-    hipLaunchKernelGGL(skinny_gemm_cols_kernel, dim3((unsigned)(a.N / 16)), dim3(64), 0, stream, a);
+    const int cus = stream_grid_cus();
+    if (4 * tiles <= cus)
+      hipLaunchKernelGGL(skinny_gemm_cols_kernel<4>, dim3((unsigned)(a.N / 4)), dim3(64), 0, stream, a);
+    else if (2 * tiles <= cus)
+      hipLaunchKernelGGL(skinny_gemm_cols_kernel<8>, dim3((unsigned)(a.N / 8)), dim3(64), 0, stream, a);
+    else
+      hipLaunchKernelGGL(skinny_gemm_cols_kernel<16>, dim3((unsigned)(a.N / 16)), dim3(64), 0, stream, a);
     return hipGetLastError();
   }
   const int cus = stream_grid_cus();
