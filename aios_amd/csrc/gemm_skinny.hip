@@ -451,12 +451,15 @@ hipError_t launch_one_tile(const LinearArgs& a, int nc, hipStream_t stream) {
 template <int PRO, int EPI>
 hipError_t launch_pe(const LinearArgs& a, int nc, hipStream_t stream) {
   if ((a.M + 15) / 16 == 1) {
-    // the decode-step shapes: K = 768, 1024, 2048 with a fixed step count
+    // the decode-step shapes: K = 768, 1024, 2048, 3072 with a fixed step count
     switch (a.K / 128) {
       case 6: return launch_one_tile<PRO, EPI, 6>(a, nc, stream);
       case 8: return launch_one_tile<PRO, EPI, 8>(a, nc, stream);
       case 16:
         if constexpr (PRO == kPlain) return launch_one_tile<PRO, EPI, 16>(a, nc, stream);
+        break;
+      case 24:  // K 3072 (the down projection of hidden-1024 models)
+        if constexpr (PRO == kPlain) return launch_one_tile<PRO, EPI, 24>(a, nc, stream);
         break;
       default: break;
     }

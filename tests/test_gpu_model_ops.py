@@ -79,7 +79,9 @@ def test_silu_and_mul(rows, inter):
                                    (8, 16384, 768), (5, 20016, 768), (16, 32768, 1024),
                                    (8, 151936, 1024),
                                    # K 2048 plain (the down projection): 8-column tiles
-                                   (1, 16, 2048), (16, 1024, 2048)])
+                                   (1, 16, 2048), (16, 1024, 2048),
+                                   # K 3072 plain (fixed step count)
+                                   (8, 1024, 3072), (3, 2560, 3072)])
 def test_linear_rows_matches_fp32_gemm(m, n, k):
     """Few-row GEMM kernel vs an fp32 matmul of the same bf16 operands: fp32
     accumulation, one bf16 rounding at the end."""
