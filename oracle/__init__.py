@@ -53,9 +53,12 @@ Modules and what pins each function (the checks live in tests/test_oracle.py):
                 closed forms (RoPE pair rotation by pos * theta^(-2i/D),
                 identity at position 0, norm preservation; with every
                 projection zeroed the logits are RMSNorm(embed) @ embed^T).
-                The Block-AttnRes trunk composition has no independent
-                implementation or reference-held fixture offline: "parity
-                unpinned" (only its mixer, attnres.py above, is pinned).
+                The Block-AttnRes trunk composition is pinned by its
+                zero-query closed form (every depth softmax uniform, so the
+                trunk at eps 1e-12 equals transformers' Qwen3 on the same
+                weights, at 8 layers in 4 blocks and 6 layers in 2 blocks;
+                a planted stale-source MLP mixer fails it by more than
+                1e-2); non-zero queries by the mixer's own known answers.
   cpu_decoder.py  KV-cached CPU decoder over the paged pool (the same
                 forward, attention by sdpa_cpu.py), bf16 or fp32: the
                 full-model leg of bench.py's CPU baseline.  Pinned against

@@ -24,8 +24,14 @@ product path does not appear here at all.
 
 Pinning: the standard trunk equals transformers' Qwen3ForCausalLM on the same
 weights (tests/test_oracle_hf.py).  The Block-AttnRes trunk composition is
-parity unpinned: no independent implementation or reference fixture of it
-exists offline.
+pinned by its zero-query closed form in the same file: with every mixer query
+zero each depth softmax is uniform, each mixer returns the standard residual
+stream divided by its source count, and since every mixer output feeds an
+RMSNorm (RMSNorm(x/S) is RMSNorm(x) with eps*S^2), the trunk at eps 1e-12
+equals transformers' Qwen3 on the same weights; a planted wiring mistake (the
+MLP mixer reading the sources without the attention delta) fails that check
+by more than 1e-2.  Non-zero queries are pinned by the mixer's known answers
+(oracle/attnres.py, tests/test_oracle.py).
 """
 from __future__ import annotations
 
