@@ -25,6 +25,9 @@ class ModelConfig:
     residual_type: str = "standard"
     attnres_num_blocks: int = 0
     attnres_alpha: float = 1.0
+    # The tokenizer's pad id (config.json "pad_token_id"); the CandidateGroup
+    # engine fills its refill ban table with it when the group config names none.
+    pad_token_id: int | None = None
 
     def __post_init__(self) -> None:
         if self.num_qo_heads % self.num_kv_heads:

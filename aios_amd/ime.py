@@ -105,7 +105,8 @@ class CandidateGroupConfig:
     refill_deadline_ms: float = 0.0  # no new round after this wall time (0: none)
     # Fill of the per-row banned-id table where no banned sequence matches
     # (ime.py:990-996 fills with the tokenizer's pad id, so during the ban
-    # window every row is also forbidden the pad id); None: no fill id.
+    # window every row is also forbidden the pad id); None: the model
+    # config's pad_token_id, and no fill id if that is None too.
     pad_token_id: int | None = None
 
     def validate(self) -> None:
@@ -458,6 +459,14 @@ class CandidateGroupEngine:
         self._prefix_logits = logits
         return logits, prefix_pages, reused
 
+    def _ban_fill(self, config: CandidateGroupConfig) -> int:
+        """The id forbidden to rows that match no ban during the ban window:
+        the group config's pad id, else the model config's, else none (-1)."""
+        pad = config.pad_token_id
+        if pad is None:
+            pad = getattr(self.rt.config, "pad_token_id", None)
+        return -1 if pad is None else int(pad)
+
     def _prefill(self, token_ids, cached_len: int, out_pages: torch.Tensor) -> torch.Tensor:
         """Prefix prefill (cached_len 0) or LCP extension (ime.py:1170-1217).
         With graphs, prefills of up to MAX_GRAPHED_PREFILL new tokens replay a
@@ -537,7 +546,7 @@ class CandidateGroupEngine:
                     ban_ids[i, : len(b)] = torch.tensor(b, dtype=torch.long, device=dev)
                 ban_lens = torch.tensor([len(b) for b in banned], dtype=torch.long, device=dev)
 
-            fill = -1 if config.pad_token_id is None else int(config.pad_token_id)
+            fill = self._ban_fill(config)
 
             def pick(logits, rows, step):
                 col = torch.full((1,), step, dtype=torch.int64, device=dev)
@@ -780,7 +789,7 @@ class _DecodeGraph:
             self.ban_cols = torch.arange(steps, dtype=torch.long, device=dev)
             self.ban_min = torch.full((1,), config.refill_ban_min_prefix_tokens,
                                       dtype=torch.long, device=dev)
-            self.ban_fill = -1 if config.pad_token_id is None else int(config.pad_token_id)
+            self.ban_fill = eng._ban_fill(config)
             self.ban_max = torch.zeros(1, dtype=torch.long, device=dev)  # longest ban
         self.tok = torch.zeros(rows, dtype=torch.long, device=dev)
         self.raw = torch.zeros(rows, dtype=torch.float32, device=dev)

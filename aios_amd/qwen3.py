@@ -119,8 +119,16 @@ class Qwen3ForCausalLM:
     def _attention(self, i: int, qkv: torch.Tensor, positions, kv_cache, batch) -> torch.Tensor:
         """qwen3.py:52-75 after the qkv projection: per-head q/k RMSNorm +
         RoPE, the backend, o_proj (v stays a strided view into qkv, as in the
-        reference).  An appending decode batch on the gfx950 ops takes the
-        norm and rotation inside the decode launch (forward_rope)."""
+        reference)."""
+        out = self.attention_core(i, qkv, positions, kv_cache, batch)
+        return self.ops.linear(out.reshape(qkv.shape[0], -1), self.w["layers"][i]["o"])
+
+    def attention_core(self, i: int, qkv: torch.Tensor, positions, kv_cache,
+                       batch) -> torch.Tensor:
+        """The attention of layer i between the qkv projection and o_proj:
+        q/k norm + RoPE and the backend call -> [T, Hq, D] (or [T, Hq*D]).
+        An appending decode batch on the gfx950 ops takes the norm and
+        rotation inside the decode launch (forward_rope)."""
         c = self.config
         lw = self.w["layers"][i]
         t = qkv.shape[0]
@@ -139,7 +147,7 @@ class Qwen3ForCausalLM:
             q, k = self.ops.qk_norm_rope(qkv, lw["q_norm"], lw["k_norm"], self.rotary.cos,
                                          self.rotary.sin, positions, hq, hkv, d, c.rms_norm_eps)
             out = be.forward(q, k, v, kv_cache, i, batch)
-        return self.ops.linear(out.reshape(t, -1), lw["o"])
+        return out
 
     def forward(self) -> torch.Tensor:
         """Decoder layers of qwen3.py:76-109: input RMSNormFused -> qkv

@@ -45,6 +45,7 @@ def config_from_hf(data: dict) -> ModelConfig:
         residual_type=data.get("residual_type", "standard"),
         attnres_num_blocks=data.get("attnres_num_blocks", 0),
         attnres_alpha=data.get("attnres_alpha", 1.0),
+        pad_token_id=data.get("pad_token_id"),
     )
 
 
@@ -60,6 +61,8 @@ def config_to_hf(c: ModelConfig) -> dict:
         "residual_type": c.residual_type, "attnres_num_blocks": c.attnres_num_blocks,
         "attnres_alpha": c.attnres_alpha,
     }
+    if c.pad_token_id is not None:
+        data["pad_token_id"] = c.pad_token_id
     if c.residual_type == "block_attnres":
         data["layers_per_attnres_block"] = c.layers_per_attnres_block
     return data

@@ -97,6 +97,94 @@ class _HostLayers:
         self.cu_k = wl.cu_k
 
 
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache (MALL), shared by the XCDs
+
+
+def _weight_bytes(w) -> int:
+    """Bytes of every tensor of a weight dict (layers included), each once."""
+    import torch
+
+    seen, total = set(), 0
+
+    def visit(x):
+        nonlocal total
+        if isinstance(x, torch.Tensor):
+            if x.data_ptr() not in seen:
+                seen.add(x.data_ptr())
+                total += x.numel() * x.element_size()
+        elif isinstance(x, dict):
+            for v in x.values():
+                visit(v)
+        elif isinstance(x, (list, tuple)):
+            for v in x:
+                visit(v)
+
+    visit(w)
+    return total
+
+
+def _decode_step_bytes(c, weights, rows: int, prefix_len: float, steps: int) -> dict:
+    """Algorithmic HBM bytes of one replayed CandidateGroup decode step,
+    averaged over the replayed steps t = 1 .. steps - 1 of a round: every
+    weight once (the tied embedding once, as the LM head), each layer's K/V
+    positions once (the shared prefix once for all rows, plus every row's t
+    own positions, the new one included), the rows' new K/V written, and the
+    bf16 logits written and read by the selection.  Activations (a few rows
+    of hidden states per layer) are left out."""
+    w_bytes = _weight_bytes(weights)
+    b_kv = 2 * c.num_kv_heads * c.head_dim * 2
+    ts = range(1, max(steps, 2))
+    kv_read = c.num_layers * b_kv * sum(prefix_len + rows * t for t in ts) / len(ts)
+    kv_write = c.num_layers * rows * b_kv
+    logits = 2 * rows * c.vocab_size * 2
+    return {"weights": int(w_bytes), "kv_read": int(kv_read), "kv_write": int(kv_write),
+            "logits": int(logits), "total": int(w_bytes + kv_read + kv_write + logits)}
+
+
+def _attention_step_us(eng, reps: int = 30) -> float:
+    """GPU time of the attention launches of one replayed decode step: the
+    q/k norm + RoPE and backend calls of every layer (what the model runs
+    between each qkv projection and o_proj), on the buffers, metadata and
+    rows of the engine's last decode graph, captured as one graph and timed
+    with HIP events over `reps` replays.  The launches run back to back here,
+    as they do between the projections of the full step."""
+    import torch
+
+    g = next(reversed(eng._graphs.values()))
+    rt = eng.rt
+    c = rt.config
+    dev = rt.device
+    width = (c.num_qo_heads + 2 * c.num_kv_heads) * c.head_dim
+    gen = torch.Generator(device=dev).manual_seed(7)
+    qkv = (torch.randn((g.rows, width), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    g.batch.out_loc = g.out_loc
+
+    def body():
+        with rt.ctx.forward_batch(g.batch):
+            for i in range(c.num_layers):
+                rt.model.attention_core(i, qkv, g.pos, rt.kv_cache, g.batch)
+
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        body()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        body()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        graph.replay()
+        e0.record(s)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    del graph
+    return us
+
+
 def _median_time(fn, warmups: int, iters: int, max_seconds: float) -> tuple[float, int]:
     """Median wall time of fn() over up to `iters` runs after `warmups`,
     stopping early (after at least 3) once `max_seconds` have passed."""
@@ -380,8 +468,11 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens=32,
     rt = CandidateGroupRuntime(c, init_weights(c, seed, "cuda"), "cuda", num_pages=2048)
     sp = None if sampling is None else SamplingParams(temperature=sampling[0], top_k=sampling[1],
                                                       top_p=sampling[2])
+    # The ban table's fill (ime.py:990-996 uses the tokenizer's pad id): id 0,
+    # the pad id of the MiniMind tokenizer, for every synthetic model here.
     cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=steps, sampling=sp, seed=seed,
-                               min_new_tokens=min_new_tokens, max_candidates=max_candidates)
+                               min_new_tokens=min_new_tokens, max_candidates=max_candidates,
+                               pad_token_id=0)
     out = {"model": f"{model}-shaped ({c.num_layers}L, {c.hidden_size}, "
                     f"{c.num_qo_heads}q/{c.num_kv_heads}kv x {c.head_dim}, "
                     f"ffn {c.intermediate_size}, vocab {c.vocab_size})",
@@ -393,7 +484,7 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens=32,
                                f"sampled: temperature {sp.temperature}, top_k {sp.top_k}, "
                                f"top_p {sp.top_p}, stateless uniforms, min_new_tokens "
                                f"{min_new_tokens}"),
-           "max_candidates": max_candidates or 8}
+           "max_candidates": max_candidates or 8, "pad_token_id": cfg.pad_token_id}
     if published:
         out["published"] = published
     for mode in ("graph", "eager"):
@@ -443,8 +534,37 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens=32,
                      "candidate_tokens_per_s": round(gen / (sum(lat) * 1e-3), 1),
                      "refill_rounds_per_run": round(rounds / runs, 3),
                      "candidates_per_run": round(attempts / runs, 2)}
+        if max_candidates > 8:
+            # adaptive legs: whether any refill round fired in the timed runs
+            out[mode]["refill_fired"] = rounds > 0
         if replayed:
-            out[mode]["replayed_step_gpu_us"] = round(replay_ms * 1e3 / replayed, 1)
+            step_us = replay_ms * 1e3 / replayed
+            out[mode]["replayed_step_gpu_us"] = round(step_us, 1)
+            if mode == "graph":
+                mean_pre = (prefix_tokens if isinstance(prefix_tokens, int)
+                            else (prefix_tokens[0] + prefix_tokens[1]) / 2) + extend
+                sb = _decode_step_bytes(c, rt.model.w, 8, mean_pre, steps)
+                attn_us = _attention_step_us(eng)
+                out["decode_step_roofline"] = {
+                    "algorithmic_bytes_per_step": sb,
+                    "replayed_step_gpu_us": round(step_us, 1),
+                    "step_hbm_gbps": round(sb["total"] / (step_us * 1e-6) / 1e9, 1),
+                    "step_roofline_frac": round(sb["total"] / (step_us * 1e-6) / 1e9
+                                                / HBM_PEAK_GBPS, 4),
+                    "weights_fit_mall": sb["weights"] <= MALL_BYTES,
+                    "attention_step_gpu_us": round(attn_us, 1),
+                    "attention_share": round(attn_us / step_us, 3),
+                    "note": ("bytes: every weight once, K/V positions once (shared prefix "
+                             "once), new K/V rows, bf16 logits written + read; mean over "
+                             "the replayed steps of an 8-row round. Weights that fit the "
+                             "256 MiB MALL may be served from it on replays, so the HBM "
+                             "fraction is then an upper-bound reading. attention: the "
+                             "q/k norm + RoPE and backend launches of every layer, replayed "
+                             "alone as one graph on the step's buffers"),
+                }
+    if max_candidates > 8 and not out["graph"].get("refill_fired", True):
+        out["note"] = ("adaptive refill: no refill round fired in the timed runs on synthetic "
+                       "weights (the first round already held 3 distinct valid candidates)")
     if published and "top3_p50_ms" in published:
         out["speedup_vs_published_p50"] = round(published["top3_p50_ms"] / out["graph"]["top3_p50_ms"], 2)
     del rt

@@ -373,7 +373,11 @@ def test_graph_prefill_matches_eager():
     graphed = CandidateGroupEngine(rt, use_graphs=True)
     eager = CandidateGroupEngine(rt, use_graphs=False)
     cfg = CandidateGroupConfig(num_candidates=8, max_new_tokens=2)
-    cases = [(5, 0), (9, 2), (9, 0), (31, 1), (5, 0), (40, 0), (70, 0), (9, 2)]
+    # (prefix, extension): the last two are the keystroke case over a longer
+    # cached prefix (KV capacity 192 and 256, device-side kv_len and indices
+    # built over the longer row)
+    cases = [(5, 0), (9, 2), (9, 0), (31, 1), (5, 0), (40, 0), (70, 0), (9, 2), (128, 2),
+             (250, 1)]
     for trial, (n, ext) in enumerate(cases):
         ids = _prefix(100 + trial, n + ext, c.vocab_size)
         res, kv = [], []
@@ -395,23 +399,31 @@ def test_graph_prefill_matches_eager():
         # the allocator hands out different pages the second time; their rows agree
         assert len(kv[0][0]) == len(kv[1][0]) == n + ext
         assert all(torch.equal(a, b) for a, b in zip(kv[0][1], kv[1][1])), (n, ext)
-    assert sorted(graphed._prefill_graphs) == [(1, 64), (2, 64), (5, 64), (9, 64), (31, 64),
-                                               (40, 64)]
+    assert sorted(graphed._prefill_graphs) == [(1, 64), (1, 256), (2, 64), (2, 192), (5, 64),
+                                               (9, 64), (31, 64), (40, 64)]
     assert not eager._prefill_graphs
     assert rt.cache_manager.available_size == rt.num_pages
 
 
 def test_graph_replay_cascade_prefix_and_neighbouring_lengths():
     """Long prefixes: the graph plans the cascade on a 64-aligned prefix and
-    serves neighbouring prefix lengths from one capture."""
+    serves neighbouring prefix lengths from one capture.  The prefixes
+    (320-350 tokens, planned prefix 320) lie above the planner's cascade
+    threshold, and the captured plan is checked to hold a cascade, so the
+    graph-replayed shared-prefix path (static metadata with prefix chunks,
+    the prefix partials and the combine, indices built on the device) stays
+    covered whatever the threshold."""
     c = replace(QWEN3_0P6B, num_layers=3, vocab_size=8192)
     eng, om = _engine(c, 12, use_graphs=True)
-    for plen in (200, 201, 230):
+    for plen in (320, 321, 350):
         prefix = _prefix(plen, plen, c.vocab_size)
         res = eng.complete(prefix, CandidateGroupConfig(num_candidates=8, max_new_tokens=6))
         _check_against_oracle(res, om, prefix, 8, 6)
         eng.reset_prefix_cache()
     assert len(eng._graphs) == 1
+    plan = next(iter(eng._graphs.values())).md.plan
+    assert plan.prefix_len == 320, plan.prefix_len
+    assert plan.num_prefix_chunks >= 1, plan.num_prefix_chunks
 
 
 def test_graph_replay_eos_masks_rows():

@@ -161,3 +161,27 @@ def test_banned_next_ids_hand_case():
     assert banned_next_ids(out, 2, bans, lens, -1).tolist() == [[7, -1], [-1, -1]]
     # step 1: both rows match ban 0's first token and ban 1's
     assert banned_next_ids(out, 1, bans, lens, 3).tolist() == [[6, 6], [6, 6]]
+
+
+def test_refill_ban_fill_defaults_to_the_model_pad_id():
+    """The refill ban table's fill (ime.py:990-996: the tokenizer's pad id)
+    comes from the group config, else from the model config's pad_token_id
+    (read from and written to config.json), else none (-1)."""
+    from dataclasses import replace
+    from types import SimpleNamespace
+
+    from aios_amd.config import MINIMIND_0P1B
+    from aios_amd.ime import CandidateGroupConfig, CandidateGroupEngine
+    from aios_amd.weights import config_from_hf, config_to_hf
+
+    fill = CandidateGroupEngine._ban_fill
+    no_pad = SimpleNamespace(rt=SimpleNamespace(config=MINIMIND_0P1B))
+    with_pad = SimpleNamespace(rt=SimpleNamespace(config=replace(MINIMIND_0P1B, pad_token_id=3)))
+    assert fill(no_pad, CandidateGroupConfig()) == -1
+    assert fill(with_pad, CandidateGroupConfig()) == 3
+    assert fill(with_pad, CandidateGroupConfig(pad_token_id=0)) == 0
+    assert fill(no_pad, CandidateGroupConfig(pad_token_id=5)) == 5
+    c = replace(MINIMIND_0P1B, pad_token_id=7)
+    assert config_from_hf(config_to_hf(c)).pad_token_id == 7
+    assert "pad_token_id" not in config_to_hf(MINIMIND_0P1B)
+    assert config_from_hf(config_to_hf(MINIMIND_0P1B)).pad_token_id is None
