@@ -166,11 +166,13 @@ def _attention_step_us(eng, reps: int = 30) -> float:
 
     s = torch.cuda.Stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(s):
-        body()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=s):
-        body()
+    # the engine's tensors are inference tensors: capture as the engine does
+    with torch.inference_mode():
+        with torch.cuda.stream(s):
+            body()
+        with torch.cuda.graph(graph, stream=s):
+            body()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(s):
