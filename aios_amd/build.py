@@ -33,6 +33,11 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-variable",
     "-Wno-unused-function",
+    # Kernel-argument preloading: the leading scalar arguments of a kernel
+    # arrive in SGPRs at wave start instead of through a load from the
+    # kernel-argument segment (the code object keeps a prologue that loads
+    # them for firmware without the feature).
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

@@ -36,12 +36,11 @@ __device__ __forceinline__ int64_t decode_rope_row(const DecodeArgs& a, int b) {
 
 // ---------------------------------------------------------------------------
 // prefix part (ROPE: the query rows are normalised and rotated on load)
-template <int D, bool ROPE>
+template <int D, int G, bool ROPE>
 __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArgs& a, int wg) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int hl = lane >> 5;
-  const int G = a.group;
   const int mg = wg % a.m_groups;
   const int unit = wg / a.m_groups;
   // Consecutive workgroups take different kv-heads: the hardware deals
@@ -127,8 +126,11 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   const int h = bh % a.num_kv_heads;
   const int b = bh / a.num_kv_heads;
 
+  // The row bounds gate everything: they go out first (cu_k is a preloaded
+  // argument).
   const int base = a.cu_k[b];
   const int kv_len = a.cu_k[b + 1] - base;
+  const bool append = a.out_loc != nullptr;  // out_loc and k_new come together
   const int s_begin = a.prefix_len + split * a.split_len;
   const int s_end = min(kv_len, s_begin + a.split_len);
 
@@ -142,25 +144,28 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   constexpr bool rope = ROPE;
   const bf16* qrow = a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + min(l16, G - 1)) * D;
   const int64_t rrow = rope ? decode_rope_row(a, b) : 0;
-  if (!rope) eng.load_q_tile(0, qrow, l16 < G);
 
   // Fused append: the row's last position is its new token, gathered from
   // k_new / v_new (page selector kNewTok) and written to its page below (no
-  // other workgroup of the launch reads that page).  A slot outside the pool
-  // is not written, and the row then attends to zeros there, as the separate
-  // append and decode would.
+  // other workgroup of the launch reads that page).  The caller's promise is
+  // that the slot out_loc[b] is the row's last page id, so the gather
+  // decides from that page id, already loaded: one outside the pool gathers
+  // zeros (the row attends to zeros there) and the slot is not written, as
+  // the separate append and decode would do.  The slot itself is needed
+  // only for the stores: it is loaded behind the first sub-tile's gathers.
   constexpr uint32_t kNoPage = 0xffffffffu;
   constexpr uint32_t kNewTok = 0xfffffffeu;
-  const int t_new = a.k_new != nullptr ? kv_len - 1 : -1;
-  const int64_t new_dst = a.k_new != nullptr ? (int64_t)a.out_loc[b] : -1;
-  const bool new_ok = (uint64_t)new_dst < (uint64_t)a.num_pages;
+  const int t_new = append ? kv_len - 1 : -1;
+  int64_t new_dst = -1;
+  bool new_ok = false;
+  bool slot_pending = append;
   const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2;
   const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2;
-  const uint8_t* kn = a.k_new != nullptr
+  const uint8_t* kn = append
                           ? reinterpret_cast<const uint8_t*>(a.k_new + (int64_t)b * a.k_new_stride +
                                                              (int64_t)h * D)
                           : g_zero_kv_row;
-  const uint8_t* vn = a.k_new != nullptr
+  const uint8_t* vn = append
                           ? reinterpret_cast<const uint8_t*>(a.v_new + (int64_t)b * a.v_new_stride +
                                                              (int64_t)h * D)
                           : g_zero_kv_row;
@@ -193,6 +198,10 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
                          : make_uint4(0u, 0u, 0u, 0u);
   };
   bool rope_pending = rope;
+  // Q goes out behind the first sub-tile's loads (it is needed only by the
+  // math; issued first, its address would wait for the kernel arguments
+  // that are not preloaded, ahead of the row bounds and page ids).
+  bool q_pending = !rope;
   const uint32_t tok_b = (uint32_t)(a.kv_tok_stride * 2);
   const uint32_t n_pages = (uint32_t)a.num_pages;
   int tok_j[NJ];
@@ -212,8 +221,10 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   for (int kv0 = s_begin + wave * kSubTok; kv0 < s_end; kv0 += NW * kSubTok) {
     const int pos = kv0 + lane;
     uint32_t sel = kNoPage;
-    if (lane < kSubTok && pos < s_end)
-      sel = pos == t_new ? (new_ok ? kNewTok : kNoPage) : (uint32_t)a.indices[base + pos];
+    if (lane < kSubTok && pos < s_end) {
+      sel = (uint32_t)a.indices[base + pos];
+      if (pos == t_new) sel = sel < n_pages ? kNewTok : kNoPage;
+    }
     // Loads whose tokens all lie past the item's end are skipped (the math
     // masks those tokens and zeroes their V fragments).
     // All page-id exchanges first: each LDS DMA rewrites M0, which waits for
@@ -232,6 +243,16 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
                            : page[j] == kNewTok ? (isv_j[j] ? vn : kn) + coff_j[j]
                                                 : g_zero_kv_row + coff_j[j];
       __builtin_amdgcn_global_load_lds(src, (AIOS_LDS void*)(buf + j * 64 * 16), 16, 0, 0);
+    }
+    if (q_pending || slot_pending) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (q_pending) eng.load_q_tile(0, qrow, l16 < G);
+      if (slot_pending) {
+        new_dst = (int64_t)a.out_loc[b];
+        new_ok = (uint64_t)new_dst < (uint64_t)a.num_pages;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      q_pending = slot_pending = false;
     }
     if (rope_pending) {
       // The rotation inputs go out right behind the sub-tile's loads and
@@ -381,15 +402,47 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   write_rows(acc, l_tot, mx, lds, a.parts.n_chunks + split, a.final_out != 0);
 }
 
+// The fields every workgroup needs before its first memory access lead the
+// kernel arguments as scalars: compiled with kernel-argument preloading they
+// arrive in SGPRs at wave start (the by-value DecodeArgs cannot be
+// preloaded, and loading it is a memory round trip ahead of the page-id
+// loads).  The copies inside DecodeArgs are overridden with them.
+struct DecodeHot {
+  const int32_t* indices;
+  const int32_t* cu_k;
+  const int32_t* out_loc;  // null: no fused append
+  int32_t prefix_wgs, prefix_len, chunk_len, m_groups, num_kv_heads, n_splits, split_len, m_rows;
+};
+__host__ __device__ inline DecodeHot decode_hot(const DecodeArgs& a) {
+  return DecodeHot{a.indices,  a.cu_k,         a.out_loc,  a.prefix_wgs, a.prefix_len, a.chunk_len,
+                   a.m_groups, a.num_kv_heads, a.n_splits, a.split_len,  a.m_rows};
+}
+
 template <int D, int G, bool ROPE>
-__global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_main_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_main_kernel(
+    const int32_t* __restrict__ indices, const int32_t* __restrict__ cu_k,
+    const int32_t* __restrict__ out_loc, int32_t prefix_wgs,
+    int32_t prefix_len, int32_t chunk_len, int32_t m_groups, int32_t num_kv_heads,
+    int32_t n_splits, int32_t split_len, int32_t m_rows, DecodeArgs args) {
   __shared__ __align__(16) uint8_t lds[KVTile<D>::LDS_BYTES];
+  DecodeArgs a = args;
+  a.indices = indices;
+  a.cu_k = cu_k;
+  a.out_loc = out_loc;
+  a.prefix_wgs = prefix_wgs;
+  a.prefix_len = prefix_len;
+  a.chunk_len = chunk_len;
+  a.m_groups = m_groups;
+  a.num_kv_heads = num_kv_heads;
+  a.n_splits = n_splits;
+  a.split_len = split_len;
+  a.m_rows = m_rows;
   // Prefix workgroups first: they carry most of the bytes, and dispatching
   // the suffix items ahead of them measured slower (their loads delay the
   // prefix streaming more than the suffix items gain).
   const int wg = blockIdx.x;
   if (wg < a.prefix_wgs) {
-    decode_prefix_part<D, ROPE>(lds, a, wg);
+    decode_prefix_part<D, G, ROPE>(lds, a, wg);
   } else {
     decode_suffix_item<D, G, ROPE>(lds, a, wg - a.prefix_wgs);
   }
@@ -418,7 +471,16 @@ __device__ __forceinline__ float wave_max(float x) {
 __device__ __forceinline__ float wave_sum(float x) { return xrow_sum(row16_sum(x)); }
 
 template <int D, int G>
-__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
+    const float* __restrict__ lse, const bf16* __restrict__ po_base, int32_t n_parts, int32_t rows,
+    int32_t num_kv_heads, DecodeArgs args) {
+  // (the leading scalars are preloaded: see decode_main_kernel)
+  DecodeArgs a = args;
+  a.parts.lse = const_cast<float*>(lse);
+  a.parts.o = const_cast<bf16*>(po_base);
+  a.parts.n_parts = n_parts;
+  a.parts.rows = rows;
+  a.num_kv_heads = num_kv_heads;
   constexpr int E8 = G * D / 8;  // 8-dim (16-byte) elements per part
   static_assert(E8 <= kCombineThreads, "one element per thread per part");
   constexpr int R = kCombineThreads / E8;  // threads sharing one element (parts split)
@@ -526,10 +588,17 @@ static hipError_t launch_main_dg(const DecodeArgs& a, hipStream_t s) {
   const int suffix_wgs = a.suffix_items;
   const dim3 grid(a.prefix_wgs + suffix_wgs);
   if (grid.x == 0) return hipSuccess;
+  const DecodeHot h = decode_hot(a);
   if (a.q_norm != nullptr)
-    hipLaunchKernelGGL((decode_main_kernel<D, G, true>), grid, dim3(kEngineThreads), 0, s, a);
+    hipLaunchKernelGGL((decode_main_kernel<D, G, true>), grid, dim3(kEngineThreads), 0, s,
+                       h.indices, h.cu_k, h.out_loc, h.prefix_wgs, h.prefix_len, h.chunk_len,
+                       h.m_groups,
+                       h.num_kv_heads, h.n_splits, h.split_len, h.m_rows, a);
   else
-    hipLaunchKernelGGL((decode_main_kernel<D, G, false>), grid, dim3(kEngineThreads), 0, s, a);
+    hipLaunchKernelGGL((decode_main_kernel<D, G, false>), grid, dim3(kEngineThreads), 0, s,
+                       h.indices, h.cu_k, h.out_loc, h.prefix_wgs, h.prefix_len, h.chunk_len,
+                       h.m_groups,
+                       h.num_kv_heads, h.n_splits, h.split_len, h.m_rows, a);
   return hipGetLastError();
 }
 
@@ -559,15 +628,22 @@ template <int D>
 static hipError_t launch_combine_d(const DecodeArgs& a, hipStream_t s) {
   const dim3 grid(a.batch * a.num_kv_heads);
   if (grid.x == 0) return hipSuccess;
+  const float* lse = a.parts.lse;
+  const bf16* po = a.parts.o;
+  const int32_t np = a.parts.n_parts, rows = a.parts.rows, hkv = a.num_kv_heads;
+#define AIOS_COMBINE(GG)                                                                      \
+  hipLaunchKernelGGL((decode_combine_kernel<D, GG>), grid, dim3(kCombineThreads), 0, s, lse, po, \
+                     np, rows, hkv, a)
   switch (a.group) {
-    case 1: hipLaunchKernelGGL((decode_combine_kernel<D, 1>), grid, dim3(kCombineThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((decode_combine_kernel<D, 2>), grid, dim3(kCombineThreads), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((decode_combine_kernel<D, 3>), grid, dim3(kCombineThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((decode_combine_kernel<D, 4>), grid, dim3(kCombineThreads), 0, s, a); break;
-    case 6: hipLaunchKernelGGL((decode_combine_kernel<D, 6>), grid, dim3(kCombineThreads), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((decode_combine_kernel<D, 8>), grid, dim3(kCombineThreads), 0, s, a); break;
+    case 1: AIOS_COMBINE(1); break;
+    case 2: AIOS_COMBINE(2); break;
+    case 3: AIOS_COMBINE(3); break;
+    case 4: AIOS_COMBINE(4); break;
+    case 6: AIOS_COMBINE(6); break;
+    case 8: AIOS_COMBINE(8); break;
     default: return hipErrorInvalidValue;
   }
+#undef AIOS_COMBINE
   return hipGetLastError();
 }
 

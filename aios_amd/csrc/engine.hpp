@@ -34,6 +34,7 @@
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "kernels.hpp"
 
@@ -199,12 +200,22 @@ __device__ __forceinline__ bf16x8 qk_rope8(const float (&xn)[8], const float (&p
 // `math(sb, kv0)` runs one sub-tile's math (ring slot at byte offset sb,
 // positions kv0 ..) and is skipped when `active` is false (a wavefront whose
 // rows are all padding only helps stream).
-// CPOL: cache policy of the gathers.
-template <class T, int CPOL, typename QLoad, typename Math>
+// CPOL: cache policy of the gathers.  ONCE: a range of at most kRing
+// sub-tiles is requested whole at the start (no ring slot is refilled) and
+// `pipe(wait_sub, n_sub)` runs the math of the whole range, calling
+// wait_sub(i) (every thread's loads of sub-tile i have landed: a wait and a
+// workgroup barrier) before it reads sub-tile i, for i = 0, 1, ... in order;
+// longer ranges, and ONCE = false, stream through the ring kLookahead
+// sub-tiles ahead with `math`.
+struct NoPipe {
+  template <typename W>
+  __device__ void operator()(W&&, int) const {}
+};
+template <class T, int CPOL, bool ONCE, typename QLoad, typename Math, typename Pipe = NoPipe>
 __device__ __forceinline__ void stream_kv(uint8_t* lds, const uint8_t* kc, const uint8_t* vc,
                                           int64_t tok_bytes, int64_t num_pages, const int32_t* idx,
                                           int kv_begin, int kv_end, QLoad&& qload, Math&& math,
-                                          bool active) {
+                                          bool active, Pipe&& pipe = Pipe{}) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int n_sub = (kv_end - kv_begin + kSubTok - 1) / kSubTok;
@@ -294,6 +305,43 @@ __device__ __forceinline__ void stream_kv(uint8_t* lds, const uint8_t* kc, const
           16, off, 0, 0, CPOL);
     }
   };
+
+  if constexpr (ONCE) {
+    static_assert(kRing == 4, "the waits below count four sub-tiles");
+    if (n_sub <= kRing) {
+      // Every sub-tile of the range goes out now (those past the range read
+      // the zero row: the range check answers them without a memory access).
+      // The chip-wide burst makes the first sub-tile land a little later
+      // than with two in flight, but the later ones land while the math of
+      // the earlier ones runs, instead of being requested only after it.
+#pragma unroll
+      for (int s = 0; s < kRing; ++s) issue(s);
+      // (called with compile-time i once the caller's loop is unrolled; the
+      // Q loads went out first, so each wait covers them too)
+      auto wait_sub = [&](int it) {
+        if (it == 0)
+          wait_vmcnt<3 * T::LPS>();
+        else if (it == 1)
+          wait_vmcnt<2 * T::LPS>();
+        else if (it == 2)
+          wait_vmcnt<T::LPS>();
+        else
+          wait_vmcnt<0>();
+        lds_barrier();  // sub-tile `it` is in LDS (every thread's share)
+      };
+      if (__builtin_amdgcn_readfirstlane((int)active)) {
+        pipe(wait_sub, n_sub);
+      } else {
+#pragma unroll
+        for (int it = 0; it < kRing; ++it) {
+          if (it >= n_sub) break;  // uniform
+          wait_sub(it);
+        }
+      }
+      wait_vmcnt<0>();  // the zero-row loads past the range have landed too
+      return;
+    }
+  }
 
   // The lookahead sub-tiles are issued unconditionally (those past the
   // range gather the zero row into ring slots nobody reads), so one wait
@@ -710,20 +758,6 @@ struct TileEngine32 {
     l_run = 0.f;
   }
 
-  template <typename QLoad>
-  __device__ void run(uint8_t* lds, const uint8_t* kc, const uint8_t* vc, int64_t tok_bytes,
-                      int64_t num_pages, const int32_t* idx, int kv_begin, int kv_end,
-                      float scale_log2, QLoad&& qload, bool active = true) {
-    reset();
-    const LaneOff lo = lane_offsets(lds);
-    // The causal (prefill) engine re-reads K/V across query tiles; the
-    // decode engine (shared prefix) streams it once.
-    stream_kv<T, CAUSAL ? 0 : kCpolStream>(
-        lds, kc, vc, tok_bytes, num_pages, idx, kv_begin, kv_end, qload,
-        [&](uint32_t sb, int kv0) { compute_at(lo, sb, kv0, kv_end, scale_log2); }, active);
-    l_run = ol[0];
-  }
-
   // LDS addresses (ring slot 0) of the lane's reads: K for each k-step; V
   // for each 32-dim tile at its first token group (the other three groups,
   // tokens +8, +16, +24, keep the slot: constant offsets).
@@ -751,6 +785,200 @@ struct TileEngine32 {
                                    (dim & 7) * 2);
     }
     return lo;
+  }
+
+  template <typename QLoad>
+  __device__ void run(uint8_t* lds, const uint8_t* kc, const uint8_t* vc, int64_t tok_bytes,
+                      int64_t num_pages, const int32_t* idx, int kv_begin, int kv_end,
+                      float scale_log2, QLoad&& qload, bool active = true) {
+    reset();
+    const LaneOff lo = lane_offsets(lds);
+    // The causal (prefill) engine re-reads K/V across query tiles; the
+    // decode engine (shared prefix) streams it once.
+    stream_kv<T, CAUSAL ? 0 : kCpolStream, !CAUSAL>(
+        lds, kc, vc, tok_bytes, num_pages, idx, kv_begin, kv_end, qload,
+        [&](uint32_t sb, int kv0) { compute_at(lo, sb, kv0, kv_end, scale_log2); }, active,
+        [&](auto&& wait_sub, int n_sub) {
+          switch (n_sub) {
+            case 1: pipe_n<1>(lo, wait_sub, kv_begin, kv_end, scale_log2); break;
+            case 2: pipe_n<2>(lo, wait_sub, kv_begin, kv_end, scale_log2); break;
+            case 3: pipe_n<3>(lo, wait_sub, kv_begin, kv_end, scale_log2); break;
+            default: pipe_n<4>(lo, wait_sub, kv_begin, kv_end, scale_log2); break;
+          }
+        });
+    l_run = ol[0];
+  }
+
+  // --- the decode math of a range resident in LDS, software-pipelined ---
+  // One sub-tile's math is three dependent steps: S^T (MFMA), the online
+  // softmax (VALU, a quarter-rate exponential per score) and O^T (MFMA).
+  // With every sub-tile of the range in LDS, iteration i runs the softmax
+  // of sub-tile i beside the S^T MFMAs of sub-tile i + 1 and the O^T MFMAs
+  // of sub-tile i - 1, three independent pieces of work, so the matrix core
+  // and the VALU run at once instead of in turn.  A moved softmax reference
+  // rescales O after the O^T update of sub-tile i - 1 (whose P was relative
+  // to the old reference).
+  __device__ __forceinline__ void read_k_at(const LaneOff& lo, uint32_t sb, bf16x8 (&kf)[KS]) const {
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      kf[s] = *reinterpret_cast<AIOS_LDS const bf16x8*>((AIOS_LDS const uint8_t*)(uintptr_t)(lo.k[s] + sb));
+  }
+  // V^T fragments by LDS transpose reads the compiler sees (so it can count
+  // them and schedule around them; its conservative wait for the ring's LDS
+  // DMAs costs little here, where every DMA went out at the start).
+  __device__ __forceinline__ void read_v_at(const LaneOff& lo, uint32_t sb, bf16x4 (&va)[NT][4]) const {
+    typedef short i16x4 __attribute__((ext_vector_type(4)));
+    auto rd = [](uint32_t addr) {
+      return __builtin_bit_cast(
+          bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((AIOS_LDS i16x4*)(uintptr_t)addr));
+    };
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const uint32_t a = lo.v[nt] + sb;
+      va[nt][0] = rd(a);
+      va[nt][1] = rd(a + 8 * T::ROWB);
+      va[nt][2] = rd(a + 16 * T::ROWB);
+      va[nt][3] = rd(a + 24 * T::ROWB);
+    }
+  }
+  __device__ __forceinline__ f32x16 mma_s_at(const bf16x8 (&kf)[KS]) const {
+    f32x16 st;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) st[i] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) st = mfma32x32x16(kf[s], qf[s], st);
+    return st;
+  }
+  // Softmax of one sub-tile's scores (positions kv0 ..): P as two bf16x8
+  // B fragments; returns whether any lane's reference moved (then `al` is
+  // the log2 of the factor its O and row sum must take, 0 for the others).
+  // MASK: positions >= kv_end may lie in this sub-tile (selects, no branch).
+  template <bool MASK>
+  __device__ __forceinline__ bool softmax_at(const f32x16& st, int kv0, int kv_end, float scale_log2,
+                                             bf16x8& pb0, bf16x8& pb1, float& al) {
+    const int h = (threadIdx.x & 63) >> 5;
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = st[r];
+    if constexpr (MASK) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        x[r] = kv0 + 8 * (r >> 2) + 4 * h + (r & 3) < kv_end ? x[r] : kNegInf;
+    }
+    float mx = vmax(vmax(vmax(vmax(x[0], x[1]), vmax(x[2], x[3])),
+                         vmax(vmax(x[4], x[5]), vmax(x[6], x[7]))),
+                    vmax(vmax(vmax(x[8], x[9]), vmax(x[10], x[11])),
+                         vmax(vmax(x[12], x[13]), vmax(x[14], x[15]))));
+    mx = xor32_max(mx) * scale_log2;
+    const bool need = mx > m_run + kRescaleSlack;
+    const bool any = __builtin_amdgcn_ballot_w64(need) != 0;
+    // (the factor, one exponential, is formed only when some lane moved)
+    al = need ? m_run - mx : 0.f;
+    m_run = need ? mx : m_run;
+    nm = need ? -mx : nm;
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(x[r], scale_log2, nm));
+    pb0 = __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                                                pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])));
+    pb1 = __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(p[8], p[9]), pack_bf16x2(p[10], p[11]),
+                                                pack_bf16x2(p[12], p[13]), pack_bf16x2(p[14], p[15])));
+    return any;
+  }
+  // O^T += V^T P^T and the row sums of P (the range's V rows past kv_end
+  // are zero rows, gathered through the -1 page ids, so no masking here).
+  __device__ __forceinline__ void mma_o_at(bf16x4 (&va)[NT][4], const bf16x8& pb0, const bf16x8& pb1) {
+    const bf16x8 ones = (bf16x8)(bf16)1.0f;
+    ol = mfma32x32x16(ones, pb0, ol);
+    ol = mfma32x32x16(ones, pb1, ol);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const bf16x8 v0 = __builtin_shufflevector(va[nt][0], va[nt][1], 0, 1, 2, 3, 4, 5, 6, 7);
+      const bf16x8 v1 = __builtin_shufflevector(va[nt][2], va[nt][3], 0, 1, 2, 3, 4, 5, 6, 7);
+      o[nt] = mfma32x32x16(v0, pb0, o[nt]);
+      o[nt] = mfma32x32x16(v1, pb1, o[nt]);
+    }
+  }
+  // O and the row sum times 2^dm (dm = old reference - new, 0 for lanes
+  // whose reference stayed).  Rare: the reference moves only when a row's
+  // max grows by more than the slack.  The empty asm keeps the compiler from
+  // speculating the 65 multiplies out of the branch that guards this call.
+  __device__ __forceinline__ void rescale(float dm) {
+    asm volatile("");
+    const float al = fast_exp2(dm);
+    ol[0] *= al;  // the other elements of ol are never read
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) o[nt] *= al;
+  }
+  // Scheduling of one pipelined iteration (one basic block): its NR LDS
+  // reads, the softmax's first VALU instructions while they land, then each MFMA
+  // followed by a few VALU instructions, so that the VALU issues while the
+  // matrix core runs.  NS / NO: the S^T / O^T MFMAs of the iteration.
+  template <int NR, int NS, int NO>
+  static __device__ __forceinline__ void interleave() {
+    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);  // every LDS read first
+    __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+    }
+  }
+  // Iteration I of N (N <= kRing sub-tiles of the range [kv_begin,
+  // kv_end)); PARTIAL: the last sub-tile may end before its 32 positions.
+  template <int N, bool PARTIAL, int I, typename WaitSub>
+  __device__ __forceinline__ void pipe_iter(const LaneOff& lo, WaitSub& wait_sub, int kv_begin,
+                                            int kv_end, float scale_log2, bf16x8 (&kf)[KS],
+                                            bf16x4 (&va)[NT][4], f32x16& st, bf16x8& pp0,
+                                            bf16x8& pp1) {
+    constexpr bool NEXT = I + 1 < N;
+    constexpr bool PREV = I > 0;
+    if constexpr (NEXT) {
+      wait_sub(I + 1);
+      read_k_at(lo, (uint32_t)((I + 1) * T::SUB_BYTES), kf);
+    }
+    if constexpr (PREV) read_v_at(lo, (uint32_t)((I - 1) * T::SUB_BYTES), va);
+    float al;
+    bf16x8 pc0, pc1;
+    const bool moved = softmax_at<PARTIAL && !NEXT>(st, kv_begin + I * kSubTok, kv_end,
+                                                    scale_log2, pc0, pc1, al);
+    if constexpr (NEXT) st = mma_s_at(kf);
+    if constexpr (PREV) mma_o_at(va, pp0, pp1);
+    interleave<(NEXT ? KS : 0) + (PREV ? 4 * NT : 0), NEXT ? KS : 0, PREV ? 2 * NT + 2 : 0>();
+    if (__builtin_expect(moved, 0)) rescale(al);
+    pp0 = pc0;
+    pp1 = pc1;
+  }
+  template <int N, bool PARTIAL, typename WaitSub, int... Is>
+  __device__ __forceinline__ void pipe_seq(const LaneOff& lo, WaitSub& wait_sub, int kv_begin,
+                                           int kv_end, float scale_log2,
+                                           std::integer_sequence<int, Is...>) {
+    static_assert(N >= 1 && N <= kRing, "range resident in the ring");
+    bf16x8 kf[KS];
+    bf16x4 va[NT][4];
+    bf16x8 pp0, pp1;
+    wait_sub(0);
+    read_k_at(lo, 0, kf);
+    f32x16 st = mma_s_at(kf);
+    (pipe_iter<N, PARTIAL, Is>(lo, wait_sub, kv_begin, kv_end, scale_log2, kf, va, st, pp0, pp1),
+     ...);
+    read_v_at(lo, (uint32_t)((N - 1) * T::SUB_BYTES), va);
+    mma_o_at(va, pp0, pp1);
+  }
+  template <int N, typename WaitSub>
+  __device__ __forceinline__ void pipe_n(const LaneOff& lo, WaitSub&& wait_sub, int kv_begin,
+                                         int kv_end, float scale_log2) {
+    if ((kv_end - kv_begin) % kSubTok == 0)
+      pipe_seq<N, false>(lo, wait_sub, kv_begin, kv_end, scale_log2,
+                         std::make_integer_sequence<int, N>{});
+    else
+      pipe_seq<N, true>(lo, wait_sub, kv_begin, kv_end, scale_log2,
+                        std::make_integer_sequence<int, N>{});
   }
 
   __device__ __forceinline__ void compute_at(const LaneOff& lo, uint32_t sb, int kv0, int kv_end,
