@@ -47,13 +47,37 @@ __device__ __forceinline__ bf16x8 pack8(const float* f) {
                          pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])));
 }
 
+// The operands every workgroup needs before its first load lead the kernel
+// arguments as scalars: compiled with kernel-argument preloading they arrive
+// in SGPRs at wave start, instead of behind a load of the kernel-argument
+// segment (LinearArgs, by value, cannot be preloaded).  The kernels then
+// override the copies inside LinearArgs with them.
+#define AIOS_LINEAR_HOT_PARAMS                                                              \
+  const bf16 *__restrict__ hx_, const bf16 *__restrict__ hw_, const bf16 *hn_, const bf16 *hr_, \
+      int32_t hxs_, int32_t hws_, int32_t hm_, int32_t hk_, int32_t hn32_, LinearArgs args_
+#define AIOS_LINEAR_HOT_ARGS(a)                                                             \
+  (a).x, (a).w, (a).norm_w, (a).residual, (int32_t)(a).x_stride, (int32_t)(a).w_stride, (a).M, \
+      (a).K, (int32_t)(a).N, (a)
+#define AIOS_LINEAR_HOT_BIND \
+  LinearArgs a = args_;      \
+  a.x = hx_;                 \
+  a.w = hw_;                 \
+  a.norm_w = hn_;            \
+  a.residual = hr_;          \
+  a.x_stride = hxs_;         \
+  a.w_stride = hws_;         \
+  a.M = hm_;                 \
+  a.K = hk_;                 \
+  a.N = hn32_;
+
 // KS > 0: the K steps of a wavefront (K / 128) fixed at compile time, so
 // the operand loads are one straight-line burst; KS = 0: read from K.
 // NC = 8 / 4: a workgroup owns 8 / 4 output columns (the MFMA tile's other W
 // rows are not loaded and read as zero), 2x / 4x the workgroups at 1/2 / 1/4
 // of the weight bytes each, for projections with few column tiles.
 template <int MT, int PRO, int EPI, int KS = 0, int NC = 16>
-__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(LinearArgs a) {
+__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_kernel(AIOS_LINEAR_HOT_PARAMS) {
+  AIOS_LINEAR_HOT_BIND
   static_assert(NC == 16 || ((NC == 8 || NC == 4) && MT == 1), "narrow tiles: one row tile");
   constexpr int NP = EPI == kSiluPair ? 2 : 1;  // W row sets per workgroup
   __shared__ f32x4 red[3][NP][MT][64];
@@ -262,7 +286,8 @@ constexpr int kRsrcWord3 = 0x00020000;  // raw buffer descriptor word 3 (32-bit 
 constexpr int kStreamMaxIters = 32;  // tiles one workgroup stages in LDS
 
 template <int PRO, int KS>
-__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_stream_kernel(LinearArgs a) {
+__global__ __launch_bounds__(kGemmThreads) void skinny_gemm_stream_kernel(AIOS_LINEAR_HOT_PARAMS) {
+  AIOS_LINEAR_HOT_BIND
   __shared__ f32x4 red[2][4][64];  // per tile parity: the four wavefronts' partials
   __shared__ float ssq[4][16];
   __shared__ uint2 out_s[kStreamMaxIters][64];  // a tile: 16 rows x 4 groups of 4 columns
@@ -397,7 +422,8 @@ constexpr int kColsSteps = 24;  // K = 768
 // NC columns per wavefront (16, or 8 / 4 with the MFMA tile's other W rows
 // read as zero, for projections with few column tiles).
 template <int NC>
-__global__ __launch_bounds__(64) void skinny_gemm_cols_kernel(LinearArgs a) {
+__global__ __launch_bounds__(64) void skinny_gemm_cols_kernel(AIOS_LINEAR_HOT_PARAMS) {
+  AIOS_LINEAR_HOT_BIND
   const int lane = threadIdx.x;
   const int l16 = lane & 15;
   const int lg = lane >> 4;
@@ -429,7 +455,7 @@ __global__ __launch_bounds__(64) void skinny_gemm_cols_kernel(LinearArgs a) {
 template <int MT, int PRO, int EPI, int KS, int NC>
 hipError_t launch_tiles(const LinearArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((skinny_gemm_kernel<MT, PRO, EPI, KS, NC>), dim3((unsigned)(a.N / NC)),
-                     dim3(kGemmThreads), 0, stream, a);
+                     dim3(kGemmThreads), 0, stream, AIOS_LINEAR_HOT_ARGS(a));
   return hipGetLastError();
 }
 
@@ -502,11 +528,14 @@ int stream_grid_cus() {
 template <int PRO, int KS>
 hipError_t launch_stream(const LinearArgs& a, int64_t grid, hipStream_t stream) {
   hipLaunchKernelGGL((skinny_gemm_stream_kernel<PRO, KS>), dim3((unsigned)grid),
-                     dim3(kGemmThreads), 0, stream, a);
+                     dim3(kGemmThreads), 0, stream, AIOS_LINEAR_HOT_ARGS(a));
   return hipGetLastError();
 }
 
 hipError_t skinny_gemm(const LinearArgs& a, int prologue, int epilogue, hipStream_t stream) {
+  // (the preloaded strides and column count are 32-bit)
+  if (a.x_stride > 0x7fffffff || a.w_stride > 0x7fffffff || a.N > 0x7fffffff)
+    return hipErrorInvalidValue;
   // Many column tiles, one row tile, K 768 / 1024: the streaming kernel,
   // when every workgroup then walks at least two tiles (and at most the
   // tiles it can stage).
@@ -525,11 +554,14 @@ hipError_t skinny_gemm(const LinearArgs& a, int prologue, int epilogue, hipStrea
   if (prologue == kPlain && epilogue == kStore && a.M <= 16 && a.K == kColsSteps * 32) {
     const int cus = stream_grid_cus();
     if (4 * tiles <= cus)
-      hipLaunchKernelGGL(skinny_gemm_cols_kernel<4>, dim3((unsigned)(a.N / 4)), dim3(64), 0, stream, a);
+      hipLaunchKernelGGL(skinny_gemm_cols_kernel<4>, dim3((unsigned)(a.N / 4)), dim3(64), 0, stream,
+                         AIOS_LINEAR_HOT_ARGS(a));
     else if (2 * tiles <= cus)
-      hipLaunchKernelGGL(skinny_gemm_cols_kernel<8>, dim3((unsigned)(a.N / 8)), dim3(64), 0, stream, a);
+      hipLaunchKernelGGL(skinny_gemm_cols_kernel<8>, dim3((unsigned)(a.N / 8)), dim3(64), 0, stream,
+                         AIOS_LINEAR_HOT_ARGS(a));
     else
-      hipLaunchKernelGGL(skinny_gemm_cols_kernel<16>, dim3((unsigned)(a.N / 16)), dim3(64), 0, stream, a);
+      hipLaunchKernelGGL(skinny_gemm_cols_kernel<16>, dim3((unsigned)(a.N / 16)), dim3(64), 0, stream,
+                         AIOS_LINEAR_HOT_ARGS(a));
     return hipGetLastError();
   }
   const int cus = stream_grid_cus();
