@@ -487,8 +487,12 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
   constexpr int NW = kCombineThreads / 64;
   constexpr int PB = (kCombineMaxParts + R - 1) / R;  // parts per thread, upper bound
   constexpr int BATCH = PB < kCombineBatch ? PB : kCombineBatch;
-  __shared__ float w_s[kCombineMaxParts * G];
-  __shared__ f32x4 red[kCombineThreads][2];
+  // Weight of part j for query row g at w_s[g][j]; the row pitch of
+  // kCombineMaxParts + 1 words keeps both the writes (a wavefront's 64 parts
+  // of one row) and the reads (the G rows of one part) free of bank conflicts.
+  constexpr int WP = kCombineMaxParts + 1;
+  __shared__ float w_s[G * WP];
+  __shared__ f32x4 red[2][kCombineThreads];  // [half][thread]: 16-byte stride, no conflicts
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -537,14 +541,14 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
       const float mu = (mx == kNegInf) ? 0.f : mx;
       const float w = lane < np ? fast_exp2(l[i] - mu) : 0.f;
       const float den = wave_sum(w);
-      w_s[lane * G + gg] = den > 0.f ? w / den : 0.f;
+      w_s[gg * WP + lane] = den > 0.f ? w / den : 0.f;
     }
   }
   __syncthreads();
 
   f32x4 acc0 = f32x4{0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
   auto fold = [&](int j, const uint4& x) {
-    const float w = w_s[j * G + g];
+    const float w = w_s[g * WP + j];
     acc0 += f32x4{lo_bf16(x.x), hi_bf16(x.x), lo_bf16(x.y), hi_bf16(x.y)} * w;
     acc1 += f32x4{lo_bf16(x.z), hi_bf16(x.z), lo_bf16(x.w), hi_bf16(x.w)} * w;
   };
@@ -562,13 +566,13 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
     for (int k = 0; k < BATCH; ++k) fold(min(j0 + k * R, kCombineMaxParts - 1), v[k]);
   }
   if (R > 1) {
-    red[tid][0] = acc0;
-    red[tid][1] = acc1;
+    red[0][tid] = acc0;
+    red[1][tid] = acc1;
     __syncthreads();
     if (r == 0)
       for (int rr = 1; rr < R; ++rr) {
-        acc0 += red[rr * E8 + e][0];
-        acc1 += red[rr * E8 + e][1];
+        acc0 += red[0][rr * E8 + e];
+        acc1 += red[1][rr * E8 + e];
       }
   }
   if (active && r == 0) {
