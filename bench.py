@@ -678,6 +678,56 @@ def attnres_pipeline(seed: int, warmups: int = 5, iters: int = 50) -> dict:
             "graph_matches_eager": matches}
 
 
+# The CandidateGroup legs, in order: (result key, candidate_group arguments).
+CANDIDATE_LEGS = [
+    # MiniMind-0.1B-shaped, greedy, 32-token prefix, 8 x 16 steps
+    ("candidate_group", {}),
+    # the same with the reference's sampled candidates (12 tokens, refill up to 12)
+    ("candidate_group_sampled",
+     dict(steps=12, sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=12)),
+    # Qwen3-0.6B-shaped: 128-token prefix extended by 2 ids (cross-keystroke
+    # reuse), 8 candidates x 24 steps.
+    ("candidate_group_qwen3_0p6b",
+     dict(model="qwen3-0.6b", prefix_tokens=128, steps=24, extend=2, runs=20, warmups=3)),
+    # Refill exercised: a greedy first round (top_k 1) yields one distinct
+    # candidate, so every run adds a refill round of 8 sampled branches.
+    ("candidate_group_refill",
+     dict(steps=12, sampling=(0.35, 1, 1.0), min_new_tokens=2, max_candidates=24, runs=10,
+          warmups=2)),
+    ("candidate_group_attnres_0p214b",
+     dict(model="minimind-attnres-0.214b", prefix_tokens=64, steps=32, runs=20, warmups=3,
+          sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=24)),
+    # C3's refill leg: a greedy first round (top_k 1) forces refill rounds
+    # of 8 sampled branches (up to 24 candidates), each of 32 steps, with
+    # the round's suffix KV freed before the next round.
+    ("candidate_group_attnres_0p214b_refill",
+     dict(model="minimind-attnres-0.214b", prefix_tokens=64, steps=32, runs=10, warmups=2,
+          sampling=(0.35, 1, 1.0), min_new_tokens=2, max_candidates=24)),
+    # The reference's published shape and contract: MiniMind-IME 0.1B
+    # (12q/4kv heads of 64, vocab 16384), 40 short prefixes ([BOS] + a
+    # few characters: 3..12 ids here), sampled T 0.35 / top_k 50 / top_p
+    # 0.9, at most 12 new tokens, first round 8, adaptive refill up to 24
+    # (README.md:120-126), and the 8 + refill (max 12) variant
+    # (reports/aios_ime_benchmark_final_20260814.md:5).
+    ("candidate_group_minimind_ime_0p1b",
+     dict(model="minimind-ime-0.1b", prefix_tokens=(3, 12), steps=12, runs=40, warmups=5,
+          sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=24,
+          published={"top3_p50_ms": 86.34, "top3_p95_ms": 99.06,
+                     "hardware": "RTX 4080 Laptop GPU, bf16",
+                     "contract": "40 frozen short prefixes, adaptive 8->24, 12 tokens",
+                     "source": "README.md:126; "
+                               "reports/aios_ime_short_prefix_matrix_20260821.md:14"})),
+    ("candidate_group_minimind_ime_0p1b_max12",
+     dict(model="minimind-ime-0.1b", prefix_tokens=(3, 12), steps=12, runs=30, warmups=5,
+          sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=12,
+          published={"top3_p50_ms": 81.98, "top3_p95_ms": 109.97,
+                     "hardware": "RTX 4080 Laptop GPU, bf16",
+                     "contract": "30 frozen prefixes, 8 + refill (max 12), 12 tokens",
+                     "source": "README.md:200; "
+                               "reports/aios_ime_benchmark_final_20260814.md:5"})),
+]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -690,9 +740,18 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=0, help="prefix chunk override (tuning)")
     ap.add_argument("--no-candidate-group", action="store_true",
                     help="skip the full-model CandidateGroup Top-3 latency")
+    ap.add_argument("--legs", default="",
+                    help="comma-separated CandidateGroup legs to run (default: all), e.g. "
+                         "candidate_group_attnres_0p214b")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
+    wanted = {x for x in args.legs.split(",") if x}
+    unknown = wanted - {name for name, _ in CANDIDATE_LEGS}
+    if unknown:
+        print(f"unknown --legs {sorted(unknown)}; the legs are "
+              f"{[name for name, _ in CANDIDATE_LEGS]}", file=sys.stderr)
+        return 2
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs the "
               "attention path on a single MI355X and does not shard across GPUs.", file=sys.stderr)
@@ -877,64 +936,14 @@ def main() -> int:
     _log(f"attnres pipeline {result['attnres_pipeline']['graph_pipeline_ms_p50']} ms (graph)")
     result["prefill"] = prefix_prefill(args.seed)
     _log(f"prefix prefill {result['prefill']['avg_launch_us']} us")
+    def want(name: str) -> bool:
+        return not wanted or name in wanted
+
     if not args.no_candidate_group:
-        result["candidate_group"] = candidate_group(args.seed)
-        _log(f"candidate group {result['candidate_group']['graph']['top3_p50_ms']} ms p50")
-        # Qwen3-0.6B-shaped: 128-token prefix extended by 2 ids (cross-keystroke
-        # reuse), 8 candidates x 24 steps.
-        result["candidate_group_sampled"] = candidate_group(
-            args.seed, steps=12, sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=12)
-        _log(f"candidate group sampled {result['candidate_group_sampled']['graph']['top3_p50_ms']} "
-             "ms p50")
-        result["candidate_group_qwen3_0p6b"] = candidate_group(
-            args.seed, model="qwen3-0.6b", prefix_tokens=128, steps=24, extend=2, runs=20,
-            warmups=3)
-        _log(f"candidate group qwen3-0.6b "
-             f"{result['candidate_group_qwen3_0p6b']['graph']['top3_p50_ms']} ms p50")
-        # Refill exercised: a greedy first round (top_k 1) yields one distinct
-        # candidate, so every run adds a refill round of 8 sampled branches.
-        result["candidate_group_refill"] = candidate_group(
-            args.seed, steps=12, sampling=(0.35, 1, 1.0), min_new_tokens=2, max_candidates=24,
-            runs=10, warmups=2)
-        _log(f"candidate group refill {result['candidate_group_refill']['graph']['top3_p50_ms']} "
-             "ms p50")
-        result["candidate_group_attnres_0p214b"] = candidate_group(
-            args.seed, model="minimind-attnres-0.214b", prefix_tokens=64, steps=32, runs=20,
-            warmups=3, sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=24)
-        _log(f"candidate group attnres-0.214b "
-             f"{result['candidate_group_attnres_0p214b']['graph']['top3_p50_ms']} ms p50")
-        # C3's refill leg: a greedy first round (top_k 1) forces refill rounds
-        # of 8 sampled branches (up to 24 candidates), each of 32 steps, with
-        # the round's suffix KV freed before the next round.
-        result["candidate_group_attnres_0p214b_refill"] = candidate_group(
-            args.seed, model="minimind-attnres-0.214b", prefix_tokens=64, steps=32, runs=10,
-            warmups=2, sampling=(0.35, 1, 1.0), min_new_tokens=2, max_candidates=24)
-        _log(f"candidate group attnres-0.214b refill "
-             f"{result['candidate_group_attnres_0p214b_refill']['graph']['top3_p50_ms']} ms p50")
-        # The reference's published shape and contract: MiniMind-IME 0.1B
-        # (12q/4kv heads of 64, vocab 16384), 40 short prefixes ([BOS] + a
-        # few characters: 3..12 ids here), sampled T 0.35 / top_k 50 / top_p
-        # 0.9, at most 12 new tokens, first round 8, adaptive refill up to 24
-        # (README.md:120-126), and the 8 + refill (max 12) variant
-        # (reports/aios_ime_benchmark_final_20260814.md:5).
-        result["candidate_group_minimind_ime_0p1b"] = candidate_group(
-            args.seed, model="minimind-ime-0.1b", prefix_tokens=(3, 12), steps=12, runs=40,
-            warmups=5, sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=24,
-            published={"top3_p50_ms": 86.34, "top3_p95_ms": 99.06,
-                       "hardware": "RTX 4080 Laptop GPU, bf16",
-                       "contract": "40 frozen short prefixes, adaptive 8->24, 12 tokens",
-                       "source": "README.md:126; reports/aios_ime_short_prefix_matrix_20260821.md:14"})
-        _log(f"candidate group minimind-ime-0.1b "
-             f"{result['candidate_group_minimind_ime_0p1b']['graph']['top3_p50_ms']} ms p50")
-        result["candidate_group_minimind_ime_0p1b_max12"] = candidate_group(
-            args.seed, model="minimind-ime-0.1b", prefix_tokens=(3, 12), steps=12, runs=30,
-            warmups=5, sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=12,
-            published={"top3_p50_ms": 81.98, "top3_p95_ms": 109.97,
-                       "hardware": "RTX 4080 Laptop GPU, bf16",
-                       "contract": "30 frozen prefixes, 8 + refill (max 12), 12 tokens",
-                       "source": "README.md:200; reports/aios_ime_benchmark_final_20260814.md:5"})
-        _log(f"candidate group minimind-ime-0.1b max12 "
-             f"{result['candidate_group_minimind_ime_0p1b_max12']['graph']['top3_p50_ms']} ms p50")
+        for name, kw in CANDIDATE_LEGS:
+            if want(name):
+                result[name] = candidate_group(args.seed, **kw)
+                _log(f"{name.replace('_', ' ')} {result[name]['graph']['top3_p50_ms']} ms p50")
     if not args.no_cpu_baseline:
         from aios_amd.workloads import OP_TEST
 
