@@ -161,6 +161,87 @@ def test_long_context_single_layer():
     np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
 
 
+def _oracle_rows(wl, layer, rows, k_cache, v_cache):
+    """Float64 oracle outputs of `rows` of one layer, over only their pages."""
+    shape = wl.shape
+    spans = [wl.indices[int(wl.cu_k[r]):int(wl.cu_k[r + 1])].long() for r in rows]
+    pages, inv = torch.unique(torch.cat(spans), return_inverse=True)
+    lens = [len(s) for s in spans]
+    cu = np.zeros(len(rows) + 1, dtype=np.int64)
+    cu[1:] = np.cumsum(lens)
+    dev_pages = pages.to(k_cache.device)
+    kc = to_np64(k_cache[layer].index_select(0, dev_pages))
+    vc = to_np64(v_cache[layer].index_select(0, dev_pages))
+    q = to_np64(wl.q[layer][list(rows)])
+    return oatt.decode_attention(q, kc, vc, inv.numpy().astype(np.int64), cu,
+                                 shape.head_dim ** -0.5)
+
+
+def test_long_context_step_every_layer():
+    # The whole 36-layer long-context step as bench.py times it: one HIP
+    # graph of 36 x (fused KV append + cascade main launch, combine),
+    # replayed twice.  Every layer's output is checked against the plain
+    # (unshared) decode of the appended caches, and two rows of every layer
+    # (all 24 rows over the 36 layers) against the float64 oracle.
+    shape = LONG_CONTEXT
+    wl = make_decode_workload(shape, seed=20260814, device=DEV, extra_token=True)
+    n, nl = shape.num_rows, shape.num_layers
+    hq, hkv, d = shape.num_qo_heads, shape.num_kv_heads, shape.head_dim
+    g = torch.Generator(device=DEV).manual_seed(20260821)
+    k_new = (torch.randn(nl, n, hkv, d, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    v_new = (torch.randn(nl, n, hkv, d, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    last = wl.indices[(wl.cu_k[1:] - 1).long()].to(DEV)
+    indices = wl.indices.to(DEV)
+    cu_k = wl.cu_k.to(DEV)
+    cu_q = torch.arange(n + 1, dtype=torch.int32)
+    main_plan = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=shape.prefix_len)
+    assert main_plan.num_prefix_chunks > 1 and main_plan.num_parts > 1
+    comb_plan = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=shape.prefix_len)
+    main_plan.stage_mask = 1
+    comb_plan.stage_mask = 2
+    ws = torch.empty(main_plan.ws_bytes, dtype=torch.uint8, device=DEV)
+    out = torch.empty(nl, n, hq, d, dtype=torch.bfloat16, device=DEV)
+    s = torch.cuda.Stream()
+    calls = []
+    for layer in range(nl):
+        calls.append(paged.bind_append_decode(main_plan, wl.q[layer], k_new[layer], v_new[layer],
+                                              last, wl.k_cache[layer], wl.v_cache[layer],
+                                              indices, cu_k, out[layer], ws, stream=s))
+        calls.append(paged.bind_decode(comb_plan, wl.q[layer], wl.k_cache[layer],
+                                       wl.v_cache[layer], indices, cu_k, out[layer], ws, stream=s))
+    graph = torch.cuda.CUDAGraph()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in calls:  # eager once (also the warm-up the capture needs)
+            c()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=s):
+        for c in calls:
+            c()
+    outs = []
+    for _ in range(2):
+        with torch.cuda.stream(s):
+            out.zero_()
+            graph.replay()
+        torch.cuda.synchronize()
+        outs.append(out.clone())
+    assert torch.equal(outs[0], outs[1])
+
+    plain = paged.plan("decode", cu_q, wl.cu_k, hq, hkv, d, shared_prefix_len=0)
+    ws_plain = torch.empty(max(plain.ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    for layer in range(nl):
+        # the appended rows are in the caches, as the step left them
+        assert torch.equal(wl.k_cache[layer][last.long()], k_new[layer])
+        assert torch.equal(wl.v_cache[layer][last.long()], v_new[layer])
+        ref = paged.decode(plain, wl.q[layer], wl.k_cache[layer], wl.v_cache[layer], indices,
+                           cu_k, workspace=ws_plain)
+        np.testing.assert_allclose(to_np64(out[layer]), to_np64(ref), **BF16_TOL)
+        rows = (layer % n, (layer + n // 2) % n)
+        np.testing.assert_allclose(to_np64(out[layer][list(rows)]),
+                                   _oracle_rows(wl, layer, rows, wl.k_cache, wl.v_cache),
+                                   **BF16_TOL)
+
+
 def test_page_permutation_invariance():
     # Relabelling physical pages (and moving their rows) must not change the output.
     wl = make_decode_workload(OP_TEST, seed=8)
