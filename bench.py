@@ -322,8 +322,8 @@ def op_test_gpu(seed: int, reps: int = 200) -> float:
 
 def cpu_baseline(host: "_HostLayers", op_host: "_HostLayers", seed: int, max_seconds: float,
                  gpu: dict) -> dict:
-    """The reference's CPU path timed on the host cores (BASELINE protocol:
-    3 warmups, median of up to 20, bf16 and fp32, same process and inputs).
+    """The reference's CPU path timed on the host cores (3 warmups, median
+    of up to 20, bf16 and fp32, same process and inputs).
 
     ``value``: the long-context decode step's attention in bf16 -- the rows
     of the first ``host.n`` layers (distinct data per layer), scaled to all

@@ -13,7 +13,7 @@ Modules and what pins each function (the checks live in tests/test_oracle.py):
                 (resources/lesson-30-triton-kv-store/run_lesson30.py:7-23) and
                 by brute-force index_put on random inputs.
   metadata.py   cu_seqlens / flat page indices / last-token rows
-                (attention/flashinfer.py:209-250 in survey numbering)
+                (attention/flashinfer.py:209-250)
                 pinned by resources/lesson-26-flashinfer-backend/run_lesson26.py
                 and resources/lesson-32-flashinfer-paged-attention/run_lesson32.py
                 known answers.

@@ -1,9 +1,9 @@
 """Oracle: batch metadata of the paged backend (test infrastructure only).
 
 Restates FlashInferAttentionBackend.prepare_metadata
-(python/aios/attention/flashinfer.py:209-250 in the survey's numbering; the
-``seqlens_q/k``, ``cu_seqlens`` and ``indices = cat(page_table[row, :len])``
-lines) and ``get_last_indices`` (:111-112).
+(python/aios/attention/flashinfer.py:209-250: the ``seqlens_q/k``,
+``cu_seqlens`` and ``indices = cat(page_table[row, :len])`` lines) and
+``get_last_indices`` (:111-112).
 """
 from __future__ import annotations
 

@@ -5,7 +5,7 @@ Tolerance: the mixer's output is bf16 and its weights are rounded to bf16
 before the sum (kernel/attnres.py:92-97); a weight whose fp32 softmax sits
 next to a bf16 rounding boundary may round the other way than in float64,
 which moves the output by up to 2^-8 of that source.  The bound is the
-north-star 1e-2 (atol and rtol); the mean error is also checked to stay at
+path's 1e-2 tolerance (atol and rtol); the mean error is also checked to stay at
 bf16 rounding level.
 """
 from __future__ import annotations
