@@ -812,33 +812,31 @@ struct TileEngine32 {
   // --- the decode math of a range resident in LDS, software-pipelined ---
   // One sub-tile's math is three dependent steps: S^T (MFMA), the online
   // softmax (VALU, a quarter-rate exponential per score) and O^T (MFMA).
-  // With every sub-tile of the range in LDS, iteration i runs the softmax
-  // of sub-tile i beside the S^T MFMAs of sub-tile i + 1 and the O^T MFMAs
-  // of sub-tile i - 1, three independent pieces of work, so the matrix core
-  // and the VALU run at once instead of in turn.  A moved softmax reference
-  // rescales O after the O^T update of sub-tile i - 1 (whose P was relative
-  // to the old reference).
+  // With every sub-tile of the range requested at once, iteration i runs
+  // the softmax of sub-tile i beside the O^T MFMAs of sub-tile i - 1 (two
+  // independent pieces of work, so the matrix core and the VALU run at once
+  // instead of in turn), then waits for sub-tile i + 1 and issues its S^T
+  // MFMAs, which the compiler schedules beside the next softmax.  A moved
+  // softmax reference rescales O after the O^T update of sub-tile i - 1
+  // (whose P was relative to the old reference).
   __device__ __forceinline__ void read_k_at(const LaneOff& lo, uint32_t sb, bf16x8 (&kf)[KS]) const {
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       kf[s] = *reinterpret_cast<AIOS_LDS const bf16x8*>((AIOS_LDS const uint8_t*)(uintptr_t)(lo.k[s] + sb));
   }
-  // V^T fragments by LDS transpose reads the compiler sees (so it can count
-  // them and schedule around them; its conservative wait for the ring's LDS
-  // DMAs costs little here, where every DMA went out at the start).
+  // V^T fragments by LDS transpose reads in inline asm, waited for in
+  // mma_o_at.  The compiler's own transpose-read builtin makes it wait for
+  // every LDS DMA still in flight (vmcnt(0)) before the first read, which
+  // held the whole pipeline behind the chunk's last sub-tile (long-context
+  // step 446 -> 442 us without it).
   __device__ __forceinline__ void read_v_at(const LaneOff& lo, uint32_t sb, bf16x4 (&va)[NT][4]) const {
-    typedef short i16x4 __attribute__((ext_vector_type(4)));
-    auto rd = [](uint32_t addr) {
-      return __builtin_bit_cast(
-          bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((AIOS_LDS i16x4*)(uintptr_t)addr));
-    };
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const uint32_t a = lo.v[nt] + sb;
-      va[nt][0] = rd(a);
-      va[nt][1] = rd(a + 8 * T::ROWB);
-      va[nt][2] = rd(a + 16 * T::ROWB);
-      va[nt][3] = rd(a + 24 * T::ROWB);
+      va[nt][0] = lds_read_tr_at<0>(a);
+      va[nt][1] = lds_read_tr_at<8 * T::ROWB>(a);
+      va[nt][2] = lds_read_tr_at<16 * T::ROWB>(a);
+      va[nt][3] = lds_read_tr_at<24 * T::ROWB>(a);
     }
   }
   __device__ __forceinline__ f32x16 mma_s_at(const bf16x8 (&kf)[KS]) const {
@@ -888,6 +886,11 @@ struct TileEngine32 {
   // O^T += V^T P^T and the row sums of P (the range's V rows past kv_end
   // are zero rows, gathered through the -1 page ids, so no masking here).
   __device__ __forceinline__ void mma_o_at(bf16x4 (&va)[NT][4], const bf16x8& pb0, const bf16x8& pb1) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      lds_wait_tied(va[nt][0], va[nt][1]);
+      lds_wait_tied(va[nt][2], va[nt][3]);
+    }
     const bf16x8 ones = (bf16x8)(bf16)1.0f;
     ol = mfma32x32x16(ones, pb0, ol);
     ol = mfma32x32x16(ones, pb1, ol);
@@ -938,19 +941,22 @@ struct TileEngine32 {
                                             bf16x8& pp1) {
     constexpr bool NEXT = I + 1 < N;
     constexpr bool PREV = I > 0;
-    if constexpr (NEXT) {
-      wait_sub(I + 1);
-      read_k_at(lo, (uint32_t)((I + 1) * T::SUB_BYTES), kf);
-    }
+    // The softmax of sub-tile I and the O^T of I - 1 need nothing new from
+    // LDS, so they go ahead of the wait for sub-tile I + 1 (still landing
+    // while they run); its K reads and S^T follow the wait.
     if constexpr (PREV) read_v_at(lo, (uint32_t)((I - 1) * T::SUB_BYTES), va);
     float al;
     bf16x8 pc0, pc1;
     const bool moved = softmax_at<PARTIAL && !NEXT>(st, kv_begin + I * kSubTok, kv_end,
                                                     scale_log2, pc0, pc1, al);
-    if constexpr (NEXT) st = mma_s_at(kf);
     if constexpr (PREV) mma_o_at(va, pp0, pp1);
-    interleave<(NEXT ? KS : 0) + (PREV ? 4 * NT : 0), NEXT ? KS : 0, PREV ? 2 * NT + 2 : 0>();
+    interleave<PREV ? 4 * NT : 0, 0, PREV ? 2 * NT + 2 : 0>();
     if (__builtin_expect(moved, 0)) rescale(al);
+    if constexpr (NEXT) {
+      wait_sub(I + 1);
+      read_k_at(lo, (uint32_t)((I + 1) * T::SUB_BYTES), kf);
+      st = mma_s_at(kf);
+    }
     pp0 = pc0;
     pp1 = pc1;
   }
