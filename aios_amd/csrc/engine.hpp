@@ -816,7 +816,7 @@ struct TileEngine32 {
   // the softmax of sub-tile i beside the O^T MFMAs of sub-tile i - 1 (two
   // independent pieces of work, so the matrix core and the VALU run at once
   // instead of in turn), then waits for sub-tile i + 1 and issues its S^T
-  // MFMAs, which the compiler schedules beside the next softmax.  A moved
+  // MFMAs, which the compiler schedules beside the softmax.  A moved
   // softmax reference rescales O after the O^T update of sub-tile i - 1
   // (whose P was relative to the old reference).
   __device__ __forceinline__ void read_k_at(const LaneOff& lo, uint32_t sb, bf16x8 (&kf)[KS]) const {
@@ -913,28 +913,6 @@ struct TileEngine32 {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) o[nt] *= al;
   }
-  // Scheduling of one pipelined iteration: NR LDS reads first (the
-  // scheduler counts only the reads it sees -- the next sub-tile's K reads,
-  // which it then moves ahead of the softmax together with their wait; the
-  // asm transpose reads are not among them), the softmax's first VALU
-  // instructions while they land, then each MFMA followed by a few VALU
-  // instructions, so that the VALU issues while the matrix core runs.
-  // NS / NO: the S^T / O^T MFMAs of the iteration.
-  template <int NR, int NS, int NO>
-  static __device__ __forceinline__ void interleave() {
-    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);  // every LDS read first
-    __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < NO; ++j) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-    }
-  }
   // Iteration I of N (N <= kRing sub-tiles of the range [kv_begin,
   // kv_end)); PARTIAL: the last sub-tile may end before its 32 positions.
   template <int N, bool PARTIAL, int I, typename WaitSub>
@@ -946,17 +924,16 @@ struct TileEngine32 {
     constexpr bool PREV = I > 0;
     // In source order the softmax of sub-tile I and the O^T of I - 1 come
     // ahead of the wait for sub-tile I + 1, and its K reads and S^T after
-    // it; the scheduling groups below let the compiler hoist the wait, the
-    // K reads and the S^T MFMAs to overlap the exponentials (measured the
-    // fastest order: long-context step 446-447 -> 438.5-439 us with the asm
-    // transpose reads, 442-443 us with the order forced).
+    // it; the compiler's own schedule then overlaps them.  Measured against
+    // forcing that order with a scheduling barrier (442-443 us per
+    // long-context step) and against `sched_group_barrier` groups of LDS
+    // reads, VALU and MFMAs (441-442 us): 437.6-439.3 us.
     if constexpr (PREV) read_v_at(lo, (uint32_t)((I - 1) * T::SUB_BYTES), va);
     float al;
     bf16x8 pc0, pc1;
     const bool moved = softmax_at<PARTIAL && !NEXT>(st, kv_begin + I * kSubTok, kv_end,
                                                     scale_log2, pc0, pc1, al);
     if constexpr (PREV) mma_o_at(va, pp0, pp1);
-    interleave<PREV ? 4 * NT : 0, 0, PREV ? 2 * NT + 2 : 0>();
     if (__builtin_expect(moved, 0)) rescale(al);
     if constexpr (NEXT) {
       wait_sub(I + 1);
