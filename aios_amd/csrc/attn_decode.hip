@@ -80,17 +80,31 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
   if (!ok) return;
   const float l_tot = eng.l_run;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  // o[nt] register 4j + i: dim 32 nt + 8j + 4h + i of the lane's row; four
-  // consecutive dims stay inside one 16-dim tile of the parts layout.
+  // o[nt] register 4j + i: dim 32 nt + 8j + 4h + i of the lane's row (h =
+  // hl: lanes l and l ^ 32 hold the two halves of each 8-dim group).  For a
+  // pair of groups (j, j + 1) the lanes swap one half each, so lane h = 0
+  // holds group j whole and lane h = 1 group j + 1: one 16-byte store per
+  // lane fills the row's 32-byte segment of a 16-dim tile, and each store
+  // instruction writes 32 rows x 32 contiguous bytes.
 #pragma unroll
   for (int nt = 0; nt < D / 32; ++nt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint2 packed;
-      packed.x = pack_bf16x2(eng.o[nt][4 * j] * inv, eng.o[nt][4 * j + 1] * inv);
-      packed.y = pack_bf16x2(eng.o[nt][4 * j + 2] * inv, eng.o[nt][4 * j + 3] * inv);
-      *reinterpret_cast<uint2*>(a.parts.o + a.parts.o_index(D, h, chunk, m, nt * 32 + 8 * j + 4 * hl)) =
-          packed;
+    for (int jp = 0; jp < 2; ++jp) {
+      const int j0 = 2 * jp, j1 = j0 + 1;
+      uint2 g0, g1;  // this lane's halves of groups j0, j1
+      g0.x = pack_bf16x2(eng.o[nt][4 * j0] * inv, eng.o[nt][4 * j0 + 1] * inv);
+      g0.y = pack_bf16x2(eng.o[nt][4 * j0 + 2] * inv, eng.o[nt][4 * j0 + 3] * inv);
+      g1.x = pack_bf16x2(eng.o[nt][4 * j1] * inv, eng.o[nt][4 * j1 + 1] * inv);
+      g1.y = pack_bf16x2(eng.o[nt][4 * j1 + 2] * inv, eng.o[nt][4 * j1 + 3] * inv);
+      // lane h = 0 sends its half of j1 and takes the partner's half of j0;
+      // lane h = 1 sends its half of j0 and takes the partner's half of j1
+      const uint2 snd = hl ? g0 : g1;
+      const auto rx = __builtin_amdgcn_permlane32_swap(snd.x, snd.x, false, false);
+      const auto ry = __builtin_amdgcn_permlane32_swap(snd.y, snd.y, false, false);
+      const uint2 rcv = hl ? make_uint2(rx[0], ry[0]) : make_uint2(rx[1], ry[1]);
+      const uint4 v = hl ? make_uint4(rcv.x, rcv.y, g1.x, g1.y) : make_uint4(g0.x, g0.y, rcv.x, rcv.y);
+      *reinterpret_cast<uint4*>(a.parts.o + a.parts.o_index(D, h, chunk, m, nt * 32 + 16 * jp + 8 * hl)) =
+          v;
     }
   if (hl == 0)
     a.parts.lse[a.parts.lse_index(h, chunk, m)] =
