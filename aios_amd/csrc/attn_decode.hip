@@ -112,6 +112,124 @@ __device__ __forceinline__ void decode_prefix_part(uint8_t* lds, const DecodeArg
 }
 
 // ---------------------------------------------------------------------------
+// Rotation on load in a suffix item, in the pair layout: eight lanes per row
+// (row 8 p + lane / 8 in pass p: the item's G query rows, then the new
+// token's K row), lane c = lane % 8 holding the P = D / 16 pairs (i, i + D/2)
+// for i in [P c, P c + P).  Each pair is rotated by the lane that holds both
+// of its dims and a row's sum of squares takes three DPP steps, so a lane
+// normalises and rotates 2 P elements per pass (12 at D = 96) with no
+// partner exchange; in the 16-row tile layout (one query row per lane of a
+// 16-lane group, G of its 16 rows live) a lane took 4 D / 16 of them plus
+// the K row's.  The rows go to the wavefront's staging area in LDS as bf16
+// and are read back as query fragments and as the K row's 16-byte chunks.
+// Arithmetic and roundings are those of qk_norm8 / qk_rope8.
+template <int D, int G>
+struct RopePairs {
+  static constexpr int P = D / 16;  // pairs per lane
+  static constexpr int W = P / 2;   // 32-bit words per half row per lane
+  static constexpr int ROWS = G + 1;
+  static constexpr int NPASS = (ROWS + 7) / 8;
+  static constexpr int STAGE_BYTES = (ROWS * D * 2 + 15) / 16 * 16;
+  static_assert(P % 2 == 0, "whole words per half row");
+  uint32_t x[NPASS][2][W], w[NPASS][2][W], c[NPASS][2][W], s[NPASS][2][W];
+
+  // q0: the item's first query row, kn: the new K row (a valid row of D
+  // bf16 either way), qw / kw: norm weights, cr / sr: the table rows of the
+  // position.  Lanes past the last row load query row 0 again (not used):
+  // the loads carry no branch.
+  __device__ __forceinline__ void load(const bf16* q0, const bf16* kn, const bf16* qw,
+                                       const bf16* kw, const bf16* cr, const bf16* sr) {
+    const int lane = threadIdx.x & 63;
+    const int c8 = lane & 7;
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int r = ps * 8 + (lane >> 3);
+      const bool isk = r == G;
+      const bf16* xs = isk ? kn : q0 + (r < G ? r : 0) * D;
+      const bf16* ws = isk ? kw : qw;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int off = hf * (D / 2) + P * c8;
+        const uint32_t* xp = reinterpret_cast<const uint32_t*>(xs + off);
+        const uint32_t* wp = reinterpret_cast<const uint32_t*>(ws + off);
+        const uint32_t* cp = reinterpret_cast<const uint32_t*>(cr + off);
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(sr + off);
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+          x[ps][hf][i] = xp[i];
+          w[ps][hf][i] = wp[i];
+          c[ps][hf][i] = cp[i];
+          s[ps][hf][i] = sp[i];
+        }
+      }
+    }
+  }
+
+  // Once the loads have landed: the rotated rows into stage ([ROWS][D] bf16).
+  __device__ __forceinline__ void finish(uint8_t* stage, float eps) const {
+    const int lane = threadIdx.x & 63;
+    const int c8 = lane & 7;
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int r = ps * 8 + (lane >> 3);
+      float xl[P], xh[P];
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        xl[2 * i] = lo_bf16(x[ps][0][i]);
+        xl[2 * i + 1] = hi_bf16(x[ps][0][i]);
+        xh[2 * i] = lo_bf16(x[ps][1][i]);
+        xh[2 * i + 1] = hi_bf16(x[ps][1][i]);
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < P; ++i) ss = fmaf(xl[i], xl[i], ss);
+#pragma unroll
+      for (int i = 0; i < P; ++i) ss = fmaf(xh[i], xh[i], ss);
+      ss = row8_sum(ss);
+      const float inv = rsqrtf(ss / (float)D + eps);
+      uint32_t yl[W], yh[W];
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        float ol[2], oh[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const uint32_t wl = w[ps][0][i], wh = w[ps][1][i];
+          const uint32_t cl = c[ps][0][i], ch = c[ps][1][i];
+          const uint32_t sl = s[ps][0][i], sh = s[ps][1][i];
+          const float nl = round_bf16(xl[2 * i + k] * inv * (k ? hi_bf16(wl) : lo_bf16(wl)));
+          const float nh = round_bf16(xh[2 * i + k] * inv * (k ? hi_bf16(wh) : lo_bf16(wh)));
+          ol[k] = round_bf16(round_bf16(nl * (k ? hi_bf16(cl) : lo_bf16(cl))) +
+                             round_bf16(-nh * (k ? hi_bf16(sl) : lo_bf16(sl))));
+          oh[k] = round_bf16(round_bf16(nh * (k ? hi_bf16(ch) : lo_bf16(ch))) +
+                             round_bf16(nl * (k ? hi_bf16(sh) : lo_bf16(sh))));
+        }
+        yl[i] = pack_bf16x2(ol[0], ol[1]);
+        yh[i] = pack_bf16x2(oh[0], oh[1]);
+      }
+      if (r < ROWS) {
+        uint32_t* dl = reinterpret_cast<uint32_t*>(stage + (r * D + P * c8) * 2);
+        uint32_t* dh = reinterpret_cast<uint32_t*>(stage + (r * D + D / 2 + P * c8) * 2);
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+          dl[i] = yl[i];
+          dh[i] = yh[i];
+        }
+      }
+    }
+  }
+};
+
+// LDS of decode_main_kernel: the prefix part's ring and page-id window, or
+// the suffix item's four sub-tile regions and the staging areas of the
+// rotation on load.
+template <int D, int G>
+constexpr int decode_lds_bytes() {
+  constexpr int a = KVTile<D>::LDS_BYTES;
+  constexpr int b = KVTile<D>::RING_BYTES + (kEngineThreads / 64) * RopePairs<D, G>::STAGE_BYTES;
+  return a > b ? a : b;
+}
+
+// ---------------------------------------------------------------------------
 // suffix part: one workgroup per (row, kv-head, split) item.  Its four
 // wavefronts take the item's 32-position sub-tiles round-robin; each gathers
 // its sub-tile of the row's own pages into its own LDS region (the engine's
@@ -150,14 +268,16 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
 
   TileEngine<D, false, 1> eng;
   eng.reset();
-  // Rotation on load (q_norm given): the row's position goes out now; the
-  // raw fragments, norm weights and cos / sin entries right behind the
-  // first sub-tile's loads (they land with them: no extra memory round
-  // trip, and nothing of them is held while those loads are issued); the
-  // norm and rotation run once they have landed.
+  // Rotation on load (q_norm given): the row's position goes out with the
+  // first sub-tile's page ids (which are waited for before the gathers
+  // anyway, so it adds no round trip); the raw rows, norm weights and cos /
+  // sin entries right behind the first sub-tile's loads (they land with
+  // them, and nothing of them is held while those loads are issued); the
+  // norm and rotation (RopePairs) run once they have landed.
   constexpr bool rope = ROPE;
-  const bf16* qrow = a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G + min(l16, G - 1)) * D;
-  const int64_t rrow = rope ? decode_rope_row(a, b) : 0;
+  const bf16* qrow0 = a.q + (int64_t)b * a.q_tok_stride + (int64_t)(h * G) * D;
+  const bf16* qrow = qrow0 + (int64_t)min(l16, G - 1) * D;
+  int32_t pos_raw = 0;
 
   // Fused append: the row's last position is its new token, gathered from
   // k_new / v_new (page selector kNewTok) and written to its page below (no
@@ -184,33 +304,15 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
                                                              (int64_t)h * D)
                           : g_zero_kv_row;
   // With the rotation on load, the new token's K row is normalised and
-  // rotated by the wavefront whose sub-tile holds it (lane c < CPR: dims
-  // 8c .. 8c + 7) together with its query rows, written over that
-  // sub-tile's loaded K row once its loads land, and to the cache page at
-  // the end.
+  // rotated (by every wavefront, with its query rows; the one whose
+  // sub-tile holds the token uses it), written over that sub-tile's loaded
+  // K row once its loads land (lane c < CPR: dims 8c .. 8c + 7), and to the
+  // cache page.
   const bool new_here =
       t_new >= s_begin && t_new < s_end && ((t_new - s_begin) / kSubTok) % NW == wave;
-  typename TileEngine<D, false, 1>::RopeIn qin;
-  bf16x8 k_x = {}, k_w = {};
-  bf16x8 k_c = {}, k_s = {};
-  auto k_rope = [&]() -> uint4 {
-    constexpr int HALF = T::CPR / 2;
-    const int c = lane & 15;
-    float x[8];
-    unpack_bf16x8(k_x, x);  // zeros past CPR
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
-    ss = row16_sum(ss);  // lanes 0 .. 15 hold the row
-    const float inv = rsqrtf(ss / (float)D + a.norm_eps);
-    qk_norm8(x, inv, k_w);
-    const int src = (lane & ~15) + (c < HALF ? c + HALF : c - HALF);
-    float p[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) p[i] = __shfl(x[i], src);
-    return lane < T::CPR ? __builtin_bit_cast(uint4, qk_rope8(x, p, c < HALF, k_c, k_s))
-                         : make_uint4(0u, 0u, 0u, 0u);
-  };
+  using RP = RopePairs<D, G>;
+  RP rp;
+  uint8_t* stage = lds + T::RING_BYTES + wave * RP::STAGE_BYTES;
   bool rope_pending = rope;
   // Q goes out behind the first sub-tile's loads (it is needed only by the
   // math; issued first, its address would wait for the kernel arguments
@@ -218,27 +320,37 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   bool q_pending = !rope;
   const uint32_t tok_b = (uint32_t)(a.kv_tok_stride * 2);
   const uint32_t n_pages = (uint32_t)a.num_pages;
-  int tok_j[NJ];
-  uint32_t coff_j[NJ];
-  bool isv_j[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int c = j * 64 + lane;
-    const bool isv = c >= CH / 2;
-    const int c2 = isv ? c - CH / 2 : c;
-    const int t = c2 / T::CPR;
-    const int slot = c2 - t * T::CPR;
-    tok_j[j] = t;
-    isv_j[j] = isv;
-    coff_j[j] = (uint32_t)((isv ? T::v_chunk(t, slot) : T::k_chunk(t, slot)) * 16);
-  }
   for (int kv0 = s_begin + wave * kSubTok; kv0 < s_end; kv0 += NW * kSubTok) {
+    // The page ids are loaded by every lane (positions past the item's end
+    // clamped to its last one, then not selected): no branch separates the
+    // row's position, loaded here too, from the page ids, so both are in
+    // flight together.
     const int pos = kv0 + lane;
-    uint32_t sel = kNoPage;
-    if (lane < kSubTok && pos < s_end) {
-      sel = (uint32_t)a.indices[base + pos];
-      if (pos == t_new) sel = sel < n_pages ? kNewTok : kNoPage;
+    const uint32_t id = (uint32_t)a.indices[base + min(pos, s_end - 1)];
+    if (rope_pending) pos_raw = a.positions[b];
+    __builtin_amdgcn_sched_barrier(0);
+    // While they are in flight: each DMA load's chunk offset in its row (the
+    // divisions by CPR included), held in registers so that none of it is
+    // recomputed between the page ids' arrival and the last load's issue.
+    // Load j and load j + NJ / 2 (K and V) cover the same tokens.
+    int tok_j[NJ / 2];
+    uint32_t coff_j[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = j * 64 + lane;
+      const bool isv = c >= CH / 2;  // the same for the whole wavefront
+      const int c2 = isv ? c - CH / 2 : c;
+      const int t = c2 / T::CPR;
+      const int slot = c2 - t * T::CPR;
+      if (!isv) tok_j[j] = t;
+      coff_j[j] = (uint32_t)((isv ? T::v_chunk(t, slot) : T::k_chunk(t, slot)) * 16);
+      asm volatile("" : "+v"(coff_j[j]));
     }
+    uint32_t sel = kNoPage;
+    if (lane < kSubTok && pos < s_end) sel = pos != t_new ? id : id < n_pages ? kNewTok : kNoPage;
+    // (the position is taken here, where it has landed with the page ids:
+    // used only behind the DMA loads, it would otherwise be loaded there)
+    if (rope_pending) asm volatile("" : "+s"(pos_raw));
     // Loads whose tokens all lie past the item's end are skipped (the math
     // masks those tokens and zeroes their V fragments).
     // All page-id exchanges first: each LDS DMA rewrites M0, which waits for
@@ -247,15 +359,19 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
     const int n_valid = __builtin_amdgcn_readfirstlane(min(s_end - kv0, kSubTok));
     uint32_t page[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) page[j] = (uint32_t)__shfl((int)sel, tok_j[j]);
+    for (int j = 0; j < NJ / 2; ++j) page[j] = page[j + NJ / 2] = (uint32_t)__shfl((int)sel, tok_j[j]);
     __builtin_amdgcn_sched_barrier(0);
+    // Each source by selects, no branch: a page of the pool, the new
+    // token's row (k_new / v_new) or the zero row.
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       if (((j * 64) % (CH / 2)) / T::CPR >= n_valid) continue;
-      const uint8_t* src = page[j] < n_pages
-                               ? (isv_j[j] ? vc : kc) + (page[j] * tok_b + coff_j[j])
-                           : page[j] == kNewTok ? (isv_j[j] ? vn : kn) + coff_j[j]
-                                                : g_zero_kv_row + coff_j[j];
+      const bool isv = j * 64 >= CH / 2;
+      const bool in_pool = page[j] < n_pages;
+      const uint8_t* rb = in_pool ? (isv ? vc : kc)
+                          : page[j] == kNewTok ? (isv ? vn : kn)
+                                               : g_zero_kv_row;
+      const uint8_t* src = rb + ((in_pool ? page[j] : 0u) * tok_b + coff_j[j]);
       __builtin_amdgcn_global_load_lds(src, (AIOS_LDS void*)(buf + j * 64 * 16), 16, 0, 0);
     }
     if (q_pending || slot_pending) {
@@ -275,16 +391,9 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
       // load counter would then hold the page ids behind the table loads)
       // or sinking them below the wait (a second round trip).
       __builtin_amdgcn_sched_barrier(0);
-      const bf16* cr = a.rope_cos + rrow * D;
-      const bf16* sr = a.rope_sin + rrow * D;
-      eng.rope_load(qin, qrow, l16 < G, a.q_norm);
-      eng.rope_tables(qin, cr, sr);
-      if (new_here && lane < T::CPR) {
-        k_x = *reinterpret_cast<const bf16x8*>(kn + lane * 16);
-        k_w = *reinterpret_cast<const bf16x8*>(a.k_norm + lane * 8);
-        k_c = *reinterpret_cast<const bf16x8*>(cr + lane * 8);
-        k_s = *reinterpret_cast<const bf16x8*>(sr + lane * 8);
-      }
+      const int64_t rrow = min(max((int64_t)pos_raw, (int64_t)0), a.rope_rows - 1);
+      rp.load(qrow0, reinterpret_cast<const bf16*>(kn), a.q_norm, a.k_norm,
+              a.rope_cos + rrow * D, a.rope_sin + rrow * D);
       __builtin_amdgcn_sched_barrier(0);
     }
     wait_vmcnt<0>();
@@ -298,9 +407,17 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
     uint4 knew = make_uint4(0u, 0u, 0u, 0u);
     bool knew_here = false;
     if (rope_pending) {
-      eng.rope_finish(0, qin, l16 < G, a.norm_eps);
+      rp.finish(stage, a.norm_eps);
+      // (the wavefront's own LDS writes, read back in order)
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s) {
+        const bf16x8 f =
+            *reinterpret_cast<const bf16x8*>(stage + (min(l16, G - 1) * D + s * 32 + lg * 8) * 2);
+        eng.qf[0][s] = l16 < G ? f : bf16x8{};
+      }
       if (new_here) {
-        knew = k_rope();
+        knew = lane < T::CPR ? *reinterpret_cast<const uint4*>(stage + (G * D + lane * 8) * 2)
+                             : make_uint4(0u, 0u, 0u, 0u);
         knew_here = true;
         if (new_ok && lane < T::CPR)
           *reinterpret_cast<uint4*>(const_cast<uint8_t*>(kc) + new_dst * tok_b + lane * 16) = knew;
@@ -438,7 +555,7 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
     const int32_t* __restrict__ out_loc, int32_t prefix_wgs,
     int32_t prefix_len, int32_t chunk_len, int32_t m_groups, int32_t num_kv_heads,
     int32_t n_splits, int32_t split_len, int32_t m_rows, DecodeArgs args) {
-  __shared__ __align__(16) uint8_t lds[KVTile<D>::LDS_BYTES];
+  __shared__ __align__(16) uint8_t lds[decode_lds_bytes<D, G>()];
   DecodeArgs a = args;
   a.indices = indices;
   a.cu_k = cu_k;

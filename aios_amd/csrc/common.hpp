@@ -76,6 +76,18 @@ __device__ __forceinline__ float row16_sum(float x) {
   x += __int_as_float(v);
   return x;
 }
+// The same within each group of 8 lanes (the first three steps: the half
+// mirror pairs lane i of a group with lane 7 - i, in its other quad).
+__device__ __forceinline__ float row8_sum(float x) {
+  int v;
+  v = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false);
+  x += __int_as_float(v);
+  v = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false);
+  x += __int_as_float(v);
+  v = __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false);
+  x += __int_as_float(v);
+  return x;
+}
 
 // Cross-row (lanes l, l^16, l^32, l^48) reductions with the gfx950 lane
 // swaps: v_permlane16_swap exchanges the odd 16-lane rows of its first

@@ -406,82 +406,6 @@ struct TileEngine {
       qf[rt][s] = ok ? *reinterpret_cast<const bf16x8*>(q + s * 32 + lg * 8) : bf16x8{};
   }
 
-  // The same fragments from the raw projection, normalised and rotated
-  // (the per-head RMSNorm + RoPE above), in three steps so that the loads of the first two can fly
-  // together with other loads: rope_load (raw fragments and norm weights),
-  // rope_tables (the cos / sin entries of the lane's dims, once the
-  // position is known), rope_finish.  Lane group lg holds dims
-  // s * 32 + lg * 8 + [0, 8) of the row, whose four lane groups sum the
-  // squares together.  A fragment's partner (dims +- D/2) is the lane's own
-  // fragment s +- KSTEPS/2 for D = 64 and 128; for D = 96 it is fragment
-  // (s + 1 + (lg >= 2)) % 3 of lane group lg ^ 2 (lane ^ 32).
-  struct RopeIn {
-    bf16x8 x[KSTEPS];
-    bf16x8 w[KSTEPS];
-    bf16x8 c[KSTEPS];
-    bf16x8 s[KSTEPS];
-  };
-  __device__ __forceinline__ void rope_load(RopeIn& in, const bf16* q, bool ok, const bf16* w) {
-    const int lg = (threadIdx.x & 63) >> 4;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      in.x[s] = ok ? *reinterpret_cast<const bf16x8*>(q + s * 32 + lg * 8) : bf16x8{};
-      in.w[s] = *reinterpret_cast<const bf16x8*>(w + s * 32 + lg * 8);
-    }
-  }
-  __device__ __forceinline__ void rope_tables(RopeIn& in, const bf16* cr, const bf16* sr) {
-    const int lg = (threadIdx.x & 63) >> 4;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      in.c[s] = *reinterpret_cast<const bf16x8*>(cr + s * 32 + lg * 8);
-      in.s[s] = *reinterpret_cast<const bf16x8*>(sr + s * 32 + lg * 8);
-    }
-  }
-  __device__ __forceinline__ void rope_finish(int rt, const RopeIn& in, bool ok, float eps) {
-    const int lane = threadIdx.x & 63;
-    const int lg = lane >> 4;
-    float x[KSTEPS][8];
-    float ss = 0.f;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      unpack_bf16x8(in.x[s], x[s]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ss = fmaf(x[s][i], x[s][i], ss);
-    }
-    ss = xrow_sum(ss);
-    const float inv = rsqrtf(ss / (float)D + eps);
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) qk_norm8(x[s], inv, in.w[s]);
-    if constexpr (D == 96) {
-      // every fragment of lane ^ 32 (v_permlane32_swap of x with itself:
-      // the first result holds lane l & 31's value, the second lane l | 32's)
-      float px[KSTEPS][8];
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[s][i]),
-                                                           __float_as_uint(x[s][i]), false, false);
-          px[s][i] = __uint_as_float(lane < 32 ? sw[1] : sw[0]);
-        }
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        const int ps = (s + 1 + (lg >= 2 ? 1 : 0)) % 3;
-        float p[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) p[i] = ps == 0 ? px[0][i] : ps == 1 ? px[1][i] : px[2][i];
-        const bool first = s * 32 + lg * 8 < D / 2;
-        qf[rt][s] = ok ? qk_rope8(x[s], p, first, in.c[s], in.s[s]) : bf16x8{};
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s)
-        qf[rt][s] = ok ? qk_rope8(x[s], x[(s + KSTEPS / 2) % KSTEPS], s < KSTEPS / 2, in.c[s],
-                                  in.s[s])
-                       : bf16x8{};
-    }
-  }
-
   __device__ __forceinline__ void reset() {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
