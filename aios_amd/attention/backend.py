@@ -405,10 +405,11 @@ class Mi355xAttentionBackend(BaseAttentionBackend):
     # Head sizes whose decoder layers take the q/k norm + rotation inside the
     # decode launch.  Measured on MI355X (graph-replayed CandidateGroup step,
     # the two forms back to back): 64 (MiniMind-IME 0.1B) 441 -> 430 us;
-    # 96 (MiniMind 0.1B) 403.3 -> 400.8 us (with the rotated K row kept out
-    # of scratch; 445 -> 445 us before); 128 (Qwen3-0.6B) 1304 -> 1339 us,
-    # its rotation inputs pushing the decode kernel past the register file.
-    ROPE_IN_DECODE_HEAD_DIMS = (64, 96)
+    # 96 (MiniMind 0.1B) 403.3 -> 400.8 us.  With the suffix items' rotation
+    # in the pair layout (half the registers of the 16-row tile layout),
+    # 128 (Qwen3-0.6B) 996 -> 981.5 us; in the tile layout it had pushed the
+    # decode kernel past the register file (1304 -> 1339 us).
+    ROPE_IN_DECODE_HEAD_DIMS = (64, 96, 128)
 
     def decode_rope_applies(self, batch: Batch) -> bool:
         """Whether forward_rope takes this batch: an appending decode batch

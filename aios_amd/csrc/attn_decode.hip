@@ -286,13 +286,14 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   // decides from that page id, already loaded: one outside the pool gathers
   // zeros (the row attends to zeros there) and the slot is not written, as
   // the separate append and decode would do.  The slot itself is needed
-  // only for the stores: it is loaded behind the first sub-tile's gathers.
+  // only for the stores: it is loaded with the first sub-tile's page ids.
   constexpr uint32_t kNoPage = 0xffffffffu;
   constexpr uint32_t kNewTok = 0xfffffffeu;
   const int t_new = append ? kv_len - 1 : -1;
   int64_t new_dst = -1;
   bool new_ok = false;
   bool slot_pending = append;
+  int32_t slot_raw = -1;
   const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.k_cache) + (int64_t)h * D * 2;
   const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.v_cache) + (int64_t)h * D * 2;
   const uint8_t* kn = append
@@ -328,6 +329,7 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
     const int pos = kv0 + lane;
     const uint32_t id = (uint32_t)a.indices[base + min(pos, s_end - 1)];
     if (rope_pending) pos_raw = a.positions[b];
+    if (slot_pending) slot_raw = a.out_loc[b];
     __builtin_amdgcn_sched_barrier(0);
     // While they are in flight: each DMA load's chunk offset in its row (the
     // divisions by CPR included), held in registers so that none of it is
@@ -348,9 +350,11 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
     }
     uint32_t sel = kNoPage;
     if (lane < kSubTok && pos < s_end) sel = pos != t_new ? id : id < n_pages ? kNewTok : kNoPage;
-    // (the position is taken here, where it has landed with the page ids:
-    // used only behind the DMA loads, it would otherwise be loaded there)
-    if (rope_pending) asm volatile("" : "+s"(pos_raw));
+    // (the position and the slot are taken here, where they have landed
+    // with the page ids: used only behind the DMA loads, they would
+    // otherwise be loaded there, one more round trip)
+    if (rope_pending) asm volatile("" : "+v"(pos_raw));
+    if (slot_pending) asm volatile("" : "+v"(slot_raw));
     // Loads whose tokens all lie past the item's end are skipped (the math
     // masks those tokens and zeroes their V fragments).
     // All page-id exchanges first: each LDS DMA rewrites M0, which waits for
@@ -378,7 +382,7 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
       __builtin_amdgcn_sched_barrier(0);
       if (q_pending) eng.load_q_tile(0, qrow, l16 < G);
       if (slot_pending) {
-        new_dst = (int64_t)a.out_loc[b];
+        new_dst = (int64_t)slot_raw;
         new_ok = (uint64_t)new_dst < (uint64_t)a.num_pages;
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -538,15 +542,24 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
 // arrive in SGPRs at wave start (the by-value DecodeArgs cannot be
 // preloaded, and loading it is a memory round trip ahead of the page-id
 // loads).  The copies inside DecodeArgs are overridden with them.
+// splits_flags carries n_splits (below 2^16: the planner bounds the parts
+// of a row at 64; the launch checks it) in its low 16 bits and
+// the suffix items' two output flags above them (final_out: bit 16,
+// wave_parts: bit 17): read only at the end, they were otherwise loaded
+// beside the row bounds, and a scalar load's wait covers every scalar load
+// in flight (they complete out of order), so they added a round trip ahead
+// of the page ids.
 struct DecodeHot {
   const int32_t* indices;
   const int32_t* cu_k;
   const int32_t* out_loc;  // null: no fused append
-  int32_t prefix_wgs, prefix_len, chunk_len, m_groups, num_kv_heads, n_splits, split_len, m_rows;
+  int32_t prefix_wgs, prefix_len, chunk_len, m_groups, num_kv_heads, splits_flags, split_len,
+      m_rows;
 };
 __host__ __device__ inline DecodeHot decode_hot(const DecodeArgs& a) {
-  return DecodeHot{a.indices,  a.cu_k,         a.out_loc,  a.prefix_wgs, a.prefix_len, a.chunk_len,
-                   a.m_groups, a.num_kv_heads, a.n_splits, a.split_len,  a.m_rows};
+  const int32_t sf = a.n_splits | (a.final_out ? 1 << 16 : 0) | (a.wave_parts ? 1 << 17 : 0);
+  return DecodeHot{a.indices,  a.cu_k,         a.out_loc, a.prefix_wgs, a.prefix_len, a.chunk_len,
+                   a.m_groups, a.num_kv_heads, sf,        a.split_len,  a.m_rows};
 }
 
 template <int D, int G, bool ROPE>
@@ -554,7 +567,7 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
     const int32_t* __restrict__ indices, const int32_t* __restrict__ cu_k,
     const int32_t* __restrict__ out_loc, int32_t prefix_wgs,
     int32_t prefix_len, int32_t chunk_len, int32_t m_groups, int32_t num_kv_heads,
-    int32_t n_splits, int32_t split_len, int32_t m_rows, DecodeArgs args) {
+    int32_t splits_flags, int32_t split_len, int32_t m_rows, DecodeArgs args) {
   __shared__ __align__(16) uint8_t lds[decode_lds_bytes<D, G>()];
   DecodeArgs a = args;
   a.indices = indices;
@@ -565,7 +578,9 @@ __global__ __launch_bounds__(kEngineThreads) __attribute__((amdgpu_waves_per_eu(
   a.chunk_len = chunk_len;
   a.m_groups = m_groups;
   a.num_kv_heads = num_kv_heads;
-  a.n_splits = n_splits;
+  a.n_splits = splits_flags & 0xffff;
+  a.final_out = (splits_flags >> 16) & 1;
+  a.wave_parts = (splits_flags >> 17) & 1;
   a.split_len = split_len;
   a.m_rows = m_rows;
   // Prefix workgroups first: they carry most of the bytes, and dispatching
@@ -723,17 +738,18 @@ static hipError_t launch_main_dg(const DecodeArgs& a, hipStream_t s) {
   const int suffix_wgs = a.suffix_items;
   const dim3 grid(a.prefix_wgs + suffix_wgs);
   if (grid.x == 0) return hipSuccess;
+  if (a.n_splits < 1 || a.n_splits >= (1 << 16)) return hipErrorInvalidValue;
   const DecodeHot h = decode_hot(a);
   if (a.q_norm != nullptr)
     hipLaunchKernelGGL((decode_main_kernel<D, G, true>), grid, dim3(kEngineThreads), 0, s,
                        h.indices, h.cu_k, h.out_loc, h.prefix_wgs, h.prefix_len, h.chunk_len,
                        h.m_groups,
-                       h.num_kv_heads, h.n_splits, h.split_len, h.m_rows, a);
+                       h.num_kv_heads, h.splits_flags, h.split_len, h.m_rows, a);
   else
     hipLaunchKernelGGL((decode_main_kernel<D, G, false>), grid, dim3(kEngineThreads), 0, s,
                        h.indices, h.cu_k, h.out_loc, h.prefix_wgs, h.prefix_len, h.chunk_len,
                        h.m_groups,
-                       h.num_kv_heads, h.n_splits, h.split_len, h.m_rows, a);
+                       h.num_kv_heads, h.splits_flags, h.split_len, h.m_rows, a);
   return hipGetLastError();
 }
 
