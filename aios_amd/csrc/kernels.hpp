@@ -19,6 +19,12 @@ struct PartsArgs {
   int32_t n_parts;
   int32_t n_chunks;
   int32_t rows;  // batch * G
+  // The struct's last word, named so that the prefix part can read it:
+  // the decode kernel loads the struct with one 8-word scalar load, and a
+  // loaded word that no code reads leaves its register free for reuse
+  // while the load is in flight, which makes the wave wait for the whole
+  // load at that reuse (ahead of the page-id loads).  Unused otherwise.
+  int32_t spare;
 
   // Element (h, j, m, d) of o for head dimension D.
   __host__ __device__ int64_t o_index(int D, int h, int j, int m, int d) const {
