@@ -711,9 +711,13 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
     acc1 += f32x4{lo_bf16(x.z), hi_bf16(x.z), lo_bf16(x.w), hi_bf16(x.w)} * w;
   };
   // Parts past the last one hold zeros and weight zero (j < kCombineMaxParts
-  // keeps every w_s read in bounds).
+  // keeps every w_s read in bounds); the unrolled fold stops at the thread's
+  // last part (the long-context rows have 36 parts: 9 of a thread's 16).
 #pragma unroll
-  for (int k = 0; k < BATCH; ++k) fold(min(r + k * R, kCombineMaxParts - 1), v[k]);
+  for (int k = 0; k < BATCH; ++k) {
+    if (r + k * R >= np) break;
+    fold(min(r + k * R, kCombineMaxParts - 1), v[k]);
+  }
   for (int j0 = r + BATCH * R; active && j0 < np; j0 += BATCH * R) {
 #pragma unroll
     for (int k = 0; k < BATCH; ++k) {
