@@ -291,9 +291,11 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   const bf16* qrow = qrow0 + (int64_t)min(l16, G - 1) * D;
   int32_t pos_raw = 0;
 
-  // Fused append: the row's last position is its new token, gathered from
-  // k_new / v_new (page selector kNewTok) and written to its page below (no
-  // other workgroup of the launch reads that page).  The caller's promise is
+  // Fused append: the row's last position is its new token, whose rows are
+  // read from k_new / v_new with its sub-tile's gathers (page selector
+  // kNewTok; the gather itself reads the zero row), written over the zero
+  // row and to its page (no other workgroup of the launch reads that
+  // page).  The caller's promise is
   // that the slot out_loc[b] is the row's last page id, so the gather
   // decides from that page id, already loaded: one outside the pool gathers
   // zeros (the row attends to zeros there) and the slot is not written, as
@@ -321,8 +323,6 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   // sub-tile holds the token uses it), written over that sub-tile's loaded
   // K row once its loads land (lane c < CPR: dims 8c .. 8c + 7), and to the
   // cache page.
-  const bool new_here =
-      t_new >= s_begin && t_new < s_end && ((t_new - s_begin) / kSubTok) % NW == wave;
   using RP = RopePairs<D, G>;
   RP rp;
   uint8_t* stage = lds + T::RING_BYTES + wave * RP::STAGE_BYTES;
@@ -331,8 +331,21 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   // math; issued first, its address would wait for the kernel arguments
   // that are not preloaded, ahead of the row bounds and page ids).
   bool q_pending = !rope;
+  // The gathers are raw-buffer LDS loads over this head's K and V rows, as
+  // in the prefix engine: the range ends with the last page's row, so a page
+  // id clamped to num_pages reads zeros by the hardware range check (page
+  // ids outside the pool, positions past the item's end, and the new token,
+  // whose rows are written into the sub-tile below), and each load's offset
+  // is one 24-bit multiply (the host keeps a layer's cache below 4 GiB and
+  // the pool below 2^24 pages) plus the chunk's offset in the row.
   const uint32_t tok_b = (uint32_t)(a.kv_tok_stride * 2);
   const uint32_t n_pages = (uint32_t)a.num_pages;
+  const int64_t n_rec64 = a.num_pages > 0 ? (a.num_pages - 1) * (int64_t)tok_b + T::ROWB : 0;
+  const int n_rec = (int)(n_rec64 < 0xffffffffll ? n_rec64 : 0xffffffffll);
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kc, (short)0, n_rec, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vc, (short)0, n_rec, kBufferWord3);
   for (int kv0 = s_begin + wave * kSubTok; kv0 < s_end; kv0 += NW * kSubTok) {
     // The page ids are loaded by every lane (positions past the item's end
     // clamped to its last one, then not selected): no branch separates the
@@ -373,22 +386,29 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
     // outstanding LDS instructions, and a load behind the exchanges would
     // also be waited for.
     const int n_valid = __builtin_amdgcn_readfirstlane(min(s_end - kv0, kSubTok));
-    uint32_t page[NJ];
+    uint32_t prow[NJ / 2];  // page byte offset of load j's token
 #pragma unroll
-    for (int j = 0; j < NJ / 2; ++j) page[j] = page[j + NJ / 2] = (uint32_t)__shfl((int)sel, tok_j[j]);
+    for (int j = 0; j < NJ / 2; ++j)
+      prow[j] = __umul24(min((uint32_t)__shfl((int)sel, tok_j[j]), n_pages), tok_b);
     __builtin_amdgcn_sched_barrier(0);
-    // Each source by selects, no branch: a page of the pool, the new
-    // token's row (k_new / v_new) or the zero row.
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       if (((j * 64) % (CH / 2)) / T::CPR >= n_valid) continue;
       const bool isv = j * 64 >= CH / 2;
-      const bool in_pool = page[j] < n_pages;
-      const uint8_t* rb = in_pool ? (isv ? vc : kc)
-                          : page[j] == kNewTok ? (isv ? vn : kn)
-                                               : g_zero_kv_row;
-      const uint8_t* src = rb + ((in_pool ? page[j] : 0u) * tok_b + coff_j[j]);
-      __builtin_amdgcn_global_load_lds(src, (AIOS_LDS void*)(buf + j * 64 * 16), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(isv ? rv : rk,
+                                               (AIOS_LDS void*)(buf + j * 64 * 16), 16,
+                                               prow[j % (NJ / 2)] + coff_j[j], 0, 0, 0);
+    }
+    // The new token's raw K / V rows (lane c < CPR: K chunk c, CPR <= c <
+    // 2 CPR: V chunk c - CPR), in flight with the gathers: written over the
+    // zero row the gathers left for it once they land, and to its page.
+    const bool new_sub = kv0 <= t_new && t_new < kv0 + kSubTok;  // uniform
+    uint4 nrow = make_uint4(0u, 0u, 0u, 0u);
+    bool new_gather = false;
+    if (new_sub) {
+      const int c = lane < T::CPR ? lane : lane < 2 * T::CPR ? lane - T::CPR : 0;
+      nrow = *reinterpret_cast<const uint4*>((lane < T::CPR ? kn : vn) + c * 16);
+      new_gather = __builtin_amdgcn_readlane((int)sel, t_new - kv0) == (int)kNewTok;
     }
     if (q_pending || slot_pending) {
       __builtin_amdgcn_sched_barrier(0);
@@ -413,15 +433,6 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
       __builtin_amdgcn_sched_barrier(0);
     }
     wait_vmcnt<0>();
-    // The rotated new K row lives only in this iteration (kept across the
-    // loop it was spilled to scratch, a memory round trip before its LDS
-    // write and another before the cache store): it goes to its cache page
-    // as soon as it is computed, and into this sub-tile if the new token
-    // is in it; a later sub-tile of this wavefront reads it back from the
-    // page (this wavefront's own store, complete after wait_vmcnt<0>; no
-    // other workgroup touches that page, so no cache holds an older copy).
-    uint4 knew = make_uint4(0u, 0u, 0u, 0u);
-    bool knew_here = false;
     if (rope_pending) {
       rp.finish(stage, a.norm_eps);
       // (the wavefront's own LDS writes, read back in order)
@@ -431,32 +442,40 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
             *reinterpret_cast<const bf16x8*>(stage + (min(l16, G - 1) * D + s * 32 + lg * 8) * 2);
         eng.qf[0][s] = l16 < G ? f : bf16x8{};
       }
-      if (new_here) {
-        knew = lane < T::CPR ? *reinterpret_cast<const uint4*>(stage + (G * D + lane * 8) * 2)
-                             : make_uint4(0u, 0u, 0u, 0u);
-        knew_here = true;
-        if (new_ok && lane < T::CPR)
-          *reinterpret_cast<uint4*>(const_cast<uint8_t*>(kc) + new_dst * tok_b + lane * 16) = knew;
-      }
       rope_pending = false;
     }
-    if (rope && new_ok && kv0 <= t_new && t_new < kv0 + kSubTok && lane < T::CPR) {
+    if (new_sub) {
+      // The rotated K row stays in the staging area (every wavefront
+      // rotated it with its query rows); the raw rows came with the
+      // gathers.  K: the rotated row where the slot is in the pool, else
+      // the raw row where the page id is; V: the raw row where the page id
+      // is (otherwise the zero row stays), as a separate append and decode
+      // would read them.  Both go to the slot's page now (no other
+      // workgroup reads that page in this launch).
       const int tl = t_new - kv0;
-      if (!knew_here) knew = *reinterpret_cast<const uint4*>(kc + new_dst * tok_b + lane * 16);
-      *reinterpret_cast<uint4*>(buf + tl * T::ROWB + T::k_slot(tl, lane) * 16) = knew;
+      const bool krot = rope && new_ok;
+      if (lane < T::CPR) {
+        // (assigned under a branch: a conditional of two lvalues is a select
+        // of their addresses, which put nrow in scratch)
+        uint4 kv = nrow;
+        if (krot) kv = *reinterpret_cast<const uint4*>(stage + (G * D + lane * 8) * 2);
+        if (krot || new_gather)
+          *reinterpret_cast<uint4*>(buf + tl * T::ROWB + T::k_slot(tl, lane) * 16) = kv;
+        if (new_ok)
+          *reinterpret_cast<uint4*>(const_cast<uint8_t*>(kc) + new_dst * tok_b + lane * 16) = kv;
+      }
+      if (lane >= T::CPR && lane < 2 * T::CPR) {
+        const int c = lane - T::CPR;
+        if (new_gather)
+          *reinterpret_cast<uint4*>(buf + T::SUB_KB + tl * T::ROWB + T::v_slot(tl, c) * 16) = nrow;
+        if (new_ok)
+          *reinterpret_cast<uint4*>(const_cast<uint8_t*>(vc) + new_dst * tok_b + c * 16) = nrow;
+      }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     eng.compute(buf, kv0, s_end, a.scale_log2, l16, lg);
   }
   eng.finish();
-
-  // The new token's rows to its page (with the rotation, K went already).
-  if (new_ok && new_here && lane < 2 * T::CPR && !(rope && lane < T::CPR)) {
-    const bool isv = lane >= T::CPR;
-    const int c = isv ? lane - T::CPR : lane;
-    const uint4 v = *reinterpret_cast<const uint4*>((isv ? vn : kn) + c * 16);
-    *reinterpret_cast<uint4*>(const_cast<uint8_t*>(isv ? vc : kc) + new_dst * tok_b + c * 16) = v;
-  }
 
   // Write the G x D rows o / l of one state: staged in LDS (the caller's
   // free region) in the order of the destination, then full-width 16-byte
