@@ -402,7 +402,9 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
     // The new token's raw K / V rows (lane c < CPR: K chunk c, CPR <= c <
     // 2 CPR: V chunk c - CPR), in flight with the gathers: written over the
     // zero row the gathers left for it once they land, and to its page.
-    const bool new_sub = kv0 <= t_new && t_new < kv0 + kSubTok;  // uniform
+    // (the item holding the token: a split item may end within a sub-tile
+    // of it)
+    const bool new_sub = kv0 <= t_new && t_new < kv0 + kSubTok && t_new < s_end;  // uniform
     uint4 nrow = make_uint4(0u, 0u, 0u, 0u);
     bool new_gather = false;
     if (new_sub) {
