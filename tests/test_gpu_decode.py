@@ -444,6 +444,17 @@ def test_append_decode_rope_matches_separate_ops(case):
         assert p.prefix_len == 140
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(8, 8, 64), (8, 8, 128), (48, 8, 96), (64, 8, 128),
+                                      (32, 4, 64)])
+def test_append_decode_rope_group_sizes(hq, hkv, d):
+    """The rotation's pair layout at the group sizes the other cases leave
+    out: G = 1 (one query row and the K row), G = 6, and G = 8, whose nine
+    rows take two passes of eight lanes per row; suffixes long enough for
+    a wavefront's second sub-tile."""
+    shape = DecodeShape(f"g{hq // hkv}_{d}", 1, 4, 60, 90, hq, hkv, d, 1024, min_suffix=40)
+    _append_decode_rope_case(shape, 31 + hq + d, shared=0)
+
+
 def test_append_decode_out_of_range_slot_matches_separate_calls():
     _append_decode_case(OP_TEST, 4, chunk=32, oob_row=3)
 
