@@ -556,6 +556,13 @@ def candidate_group(seed: int, model: str = "minimind-0.1b", prefix_tokens=32,
                     "weights_fit_mall": sb["weights"] <= MALL_BYTES,
                     "attention_step_gpu_us": round(attn_us, 1),
                     "attention_share": round(attn_us / step_us, 3),
+                    "bound": "launch latency",
+                    "bound_note": ("a decode step is a chain of dependent launches, several "
+                                   "per layer (projections, attention, depth mixers), each "
+                                   "moving 0.1-2 MB: at 8 TB/s under 0.3 us, well below the "
+                                   "~1.8 us a graph-replayed launch takes even when empty, so "
+                                   "the step time is the chain of launch latencies and round "
+                                   "trips, not HBM bandwidth"),
                     "note": ("bytes: every weight once, K/V positions once (shared prefix "
                              "once), new K/V rows, bf16 logits written + read; mean over "
                              "the replayed steps of an 8-row round. Weights that fit the "
