@@ -292,15 +292,15 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   int32_t pos_raw = 0;
 
   // Fused append: the row's last position is its new token, whose rows are
-  // read from k_new / v_new with its sub-tile's gathers (page selector
-  // kNewTok; the gather itself reads the zero row), written over the zero
-  // row and to its page (no other workgroup of the launch reads that
-  // page).  The caller's promise is
-  // that the slot out_loc[b] is the row's last page id, so the gather
-  // decides from that page id, already loaded: one outside the pool gathers
-  // zeros (the row attends to zeros there) and the slot is not written, as
-  // the separate append and decode would do.  The slot itself is needed
-  // only for the stores: it is loaded with the first sub-tile's page ids.
+  // read from k_new / v_new beside its sub-tile's gathers (page selector
+  // kNewTok; the gather itself reads the zero row), then written over the
+  // zero row and to its page (no other workgroup of the launch reads that
+  // page).  The caller's promise is that the slot out_loc[b] is the row's
+  // last page id, so whether the rows enter the sub-tile is decided from
+  // that page id, already loaded: one outside the pool leaves the zero row
+  // (the row attends to zeros there) and the slot is not written, as the
+  // separate append and decode would do.  The slot itself is needed only
+  // for the stores: it is loaded with the first sub-tile's page ids.
   constexpr uint32_t kNoPage = 0xffffffffu;
   constexpr uint32_t kNewTok = 0xfffffffeu;
   const int t_new = append ? kv_len - 1 : -1;
@@ -487,13 +487,13 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
   auto write_rows = [&](const f32x4 (&acc)[DT], float l_tot, float m, uint8_t* stage_buf,
                         int part, bool final) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    bf16* stage = reinterpret_cast<bf16*>(stage_buf);
+    bf16* srows = reinterpret_cast<bf16*>(stage_buf);
     if (l16 < G) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const f32x4 v = acc[dt] * inv;
         const int e = final ? l16 * D + dt * 16 + lg * 4 : (dt * G + l16) * 16 + lg * 4;
-        *reinterpret_cast<uint2*>(stage + e) = make_uint2(pack_bf16x2(v[0], v[1]),
+        *reinterpret_cast<uint2*>(srows + e) = make_uint2(pack_bf16x2(v[0], v[1]),
                                                          pack_bf16x2(v[2], v[3]));
       }
     }
@@ -501,7 +501,7 @@ __device__ __forceinline__ void decode_suffix_item(uint8_t* lds, const DecodeArg
     // complete in order.
     constexpr int NCH = G * D / 8;  // 16-byte chunks of the rows
     for (int c = lane; c < NCH; c += 64) {
-      const uint4 v = reinterpret_cast<const uint4*>(stage)[c];
+      const uint4 v = reinterpret_cast<const uint4*>(srows)[c];
       bf16* dst;
       if (final) {
         dst = a.out + ((int64_t)b * a.num_qo_heads + h * G) * D + c * 8;
