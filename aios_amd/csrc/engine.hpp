@@ -602,6 +602,14 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b,
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Sum of 16 values as a balanced tree (four levels of independent adds).
+__device__ __forceinline__ float sum16(const float (&p)[16]) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = p[2 * i] + p[2 * i + 1];
+  return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+}
+
 // The tile engine with one 32-row tile per wavefront and
 // v_mfma_f32_32x32x16_bf16: the same math as TileEngine<D, CAUSAL, 2> (32
 // rows per wavefront, 128 per workgroup) with half the MFMA instructions
@@ -628,7 +636,13 @@ struct TileEngine32 {
 
   bf16x8 qf[KS];
   f32x16 o[NT];
-  f32x16 ol;       // row sums of P by MFMA (element 0 is read)
+  // Row sums of P.  CAUSAL (the prefill, whose VALU is the busier pipe): by
+  // MFMA with a ones operand (element 0 is read; 4096-token prefill 166-169
+  // us with the VALU sums below instead); otherwise the lane's sum over its
+  // half of the row's positions, the halves added at the end (long-context
+  // decode step 432.5-433.1 -> 429.8-430.5 us against the MFMA sums).
+  f32x16 ol;
+  float ls;
   float m_run;     // the lane's row reference (log2 domain)
   float nm;        // -(m_run, or 0 while m_run is -inf)
   float l_run;     // row total, set by finish()
@@ -677,6 +691,7 @@ struct TileEngine32 {
       for (int i = 0; i < 16; ++i) o[t][i] = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) ol[i] = 0.f;
+    ls = 0.f;
     m_run = kNegInf;
     nm = 0.f;
     l_run = 0.f;
@@ -730,7 +745,9 @@ struct TileEngine32 {
             default: pipe_n<4>(lo, wait_sub, kv_begin, kv_end, scale_log2); break;
           }
         });
-    l_run = ol[0];
+    // (lanes l and l ^ 32 hold the two halves of a row)
+    if constexpr (CAUSAL) l_run = ol[0];
+    else l_run = xor32_sum(ls);
   }
 
   // --- the decode math of a range resident in LDS, software-pipelined ---
@@ -777,7 +794,7 @@ struct TileEngine32 {
   // MASK: positions >= kv_end may lie in this sub-tile (selects, no branch).
   template <bool MASK>
   __device__ __forceinline__ bool softmax_at(const f32x16& st, int kv0, int kv_end, float scale_log2,
-                                             bf16x8& pb0, bf16x8& pb1, float& al) {
+                                             bf16x8& pb0, bf16x8& pb1, float& al, float& psum) {
     const int h = (threadIdx.x & 63) >> 5;
     float x[16];
 #pragma unroll
@@ -801,23 +818,21 @@ struct TileEngine32 {
     float p[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(x[r], scale_log2, nm));
+    psum = sum16(p);
     pb0 = __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
                                                 pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])));
     pb1 = __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(p[8], p[9]), pack_bf16x2(p[10], p[11]),
                                                 pack_bf16x2(p[12], p[13]), pack_bf16x2(p[14], p[15])));
     return any;
   }
-  // O^T += V^T P^T and the row sums of P (the range's V rows past kv_end
-  // are zero rows, gathered through the -1 page ids, so no masking here).
+  // O^T += V^T P^T (the range's V rows past kv_end are zero rows, gathered
+  // through the -1 page ids, so no masking here).
   __device__ __forceinline__ void mma_o_at(bf16x4 (&va)[NT][4], const bf16x8& pb0, const bf16x8& pb1) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       lds_wait_tied(va[nt][0], va[nt][1]);
       lds_wait_tied(va[nt][2], va[nt][3]);
     }
-    const bf16x8 ones = (bf16x8)(bf16)1.0f;
-    ol = mfma32x32x16(ones, pb0, ol);
-    ol = mfma32x32x16(ones, pb1, ol);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const bf16x8 v0 = __builtin_shufflevector(va[nt][0], va[nt][1], 0, 1, 2, 3, 4, 5, 6, 7);
@@ -831,9 +846,10 @@ struct TileEngine32 {
   // max grows by more than the slack.  The empty asm keeps the compiler from
   // speculating the 65 multiplies out of the branch that guards this call.
   __device__ __forceinline__ void rescale(float dm) {
+    static_assert(!CAUSAL, "the pipelined decode path keeps the VALU row sums");
     asm volatile("");
     const float al = fast_exp2(dm);
-    ol[0] *= al;  // the other elements of ol are never read
+    ls *= al;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) o[nt] *= al;
   }
@@ -853,12 +869,13 @@ struct TileEngine32 {
     // long-context step) and against `sched_group_barrier` groups of LDS
     // reads, VALU and MFMAs (441-442 us): 437.6-439.3 us.
     if constexpr (PREV) read_v_at(lo, (uint32_t)((I - 1) * T::SUB_BYTES), va);
-    float al;
+    float al, psum;
     bf16x8 pc0, pc1;
     const bool moved = softmax_at<PARTIAL && !NEXT>(st, kv_begin + I * kSubTok, kv_end,
-                                                    scale_log2, pc0, pc1, al);
+                                                    scale_log2, pc0, pc1, al, psum);
     if constexpr (PREV) mma_o_at(va, pp0, pp1);
     if (__builtin_expect(moved, 0)) rescale(al);
+    ls += psum;  // (after the rescale: psum is relative to the new reference)
     if constexpr (NEXT) {
       wait_sub(I + 1);
       read_k_at(lo, (uint32_t)((I + 1) * T::SUB_BYTES), kf);
@@ -945,7 +962,8 @@ struct TileEngine32 {
     const bool need = mx > m_run + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(need)) {
       const float al = need ? fast_exp2(m_run - mx) : 1.f;
-      ol[0] *= al;  // the other elements of ol are never read
+      if constexpr (CAUSAL) ol[0] *= al;  // the other elements of ol are never read
+      else ls *= al;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) o[nt] *= al;
       m_run = need ? mx : m_run;
@@ -954,6 +972,7 @@ struct TileEngine32 {
     float p[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(x[r], scale_log2, nm));
+    if constexpr (!CAUSAL) ls += sum16(p);
     const bf16x8 pb0 = __builtin_bit_cast(
         bf16x8, make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
                            pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])));
@@ -981,10 +1000,12 @@ struct TileEngine32 {
           va[nt][q] = __builtin_bit_cast(bf16x4, __builtin_bit_cast(uint64_t, va[nt][q]) & keep);
       }
     }
-    const bf16x8 ones = (bf16x8)(bf16)1.0f;
-    if constexpr (CAUSAL) __builtin_amdgcn_s_setprio(1);
-    ol = mfma32x32x16(ones, pb0, ol);
-    ol = mfma32x32x16(ones, pb1, ol);
+    if constexpr (CAUSAL) {
+      const bf16x8 ones = (bf16x8)(bf16)1.0f;
+      __builtin_amdgcn_s_setprio(1);
+      ol = mfma32x32x16(ones, pb0, ol);
+      ol = mfma32x32x16(ones, pb1, ol);
+    }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const bf16x8 v0 = __builtin_shufflevector(va[nt][0], va[nt][1], 0, 1, 2, 3, 4, 5, 6, 7);
