@@ -242,6 +242,36 @@ def test_long_context_step_every_layer():
                                    **BF16_TOL)
 
 
+@pytest.mark.parametrize("rows,hq,hkv,d,prefix,shared", [(24, 32, 8, 128, 1024, True),
+                                                          (16, 16, 8, 128, 512, True),
+                                                          (8, 8, 2, 96, 300, True),
+                                                          (6, 32, 8, 128, 700, False)])
+def test_growing_logits_move_the_softmax_reference(rows, hq, hkv, d, prefix, shared):
+    # K rows scaled up along the positions (x1 at position 0 to x51 at the
+    # longest row's end) make a row's running max grow by ~60 log2 units, so
+    # the softmax reference moves several times inside the prefix chunks
+    # (each move rescales O and the row sums) instead of only at the first
+    # sub-tile, as it does with unit-scale data.
+    shape = DecodeShape("growing", 1, rows, prefix, 64, hq, hkv, d, 8192)
+    wl = make_decode_workload(shape, seed=20260903 + rows)
+    kv_max = int((wl.cu_k[1:] - wl.cu_k[:-1]).max())
+    scale = torch.ones(shape.num_pages)
+    for b in range(rows):
+        lo, hi = int(wl.cu_k[b]), int(wl.cu_k[b + 1])
+        pos = torch.arange(hi - lo, dtype=torch.float32)
+        scale[wl.indices[lo:hi].long()] = 1.0 + 50.0 * pos / kv_max
+    wl.k_cache = (wl.k_cache.float() * scale.view(1, -1, 1, 1)).to(torch.bfloat16)
+    out, p = _run(wl, shared=None if shared else 0)
+    assert (p.num_prefix_chunks > 1) == shared
+    # row 0's running max (log2 units, its first query head) climbs by
+    # more than twice the reference's 2^8 slack along its positions
+    idx0 = wl.indices[int(wl.cu_k[0]):int(wl.cu_k[1])].long()
+    sc = to_np64(wl.k_cache[0][idx0, 0]) @ to_np64(wl.q[0][0, 0]) * d ** -0.5 * np.log2(np.e)
+    run = np.maximum.accumulate(sc)
+    assert run[-1] - run[0] > 16.0
+    np.testing.assert_allclose(to_np64(out), _oracle(wl), **BF16_TOL)
+
+
 def test_page_permutation_invariance():
     # Relabelling physical pages (and moving their rows) must not change the output.
     wl = make_decode_workload(OP_TEST, seed=8)

@@ -104,3 +104,20 @@ def test_long_prefill_sampled_rows():
     for i in rows:
         ref = oatt.attention_one(qn[i : i + 1], kn[: i + 1], vn[: i + 1], i, d ** -0.5)
         np.testing.assert_allclose(got[i : i + 1], ref, **BF16_TOL)
+
+
+@pytest.mark.parametrize("q_lens,kv_lens,hq,hkv,d", [([512], [512], 32, 8, 128),
+                                                     ([2, 300], [130, 600], 16, 8, 128),
+                                                     ([200], [200], 8, 2, 96)])
+def test_growing_logits_move_the_softmax_reference(q_lens, kv_lens, hq, hkv, d):
+    # K rows scaled up along each request's positions (x1 to x51): a query
+    # row's running max keeps growing over its causal range, so the
+    # reference moves mid-stream and rescales O and the MFMA row sums.
+    q, kc, vc, idx, cu_q, cu_k = _make(q_lens, kv_lens, hq, hkv, d, 4096, seed=29)
+    scale = torch.ones(kc.shape[0])
+    for r in range(len(kv_lens)):
+        lo, hi = int(cu_k[r]), int(cu_k[r + 1])
+        scale[idx[lo:hi].long()] = 1.0 + 50.0 * torch.arange(hi - lo, dtype=torch.float32) / (hi - lo)
+    kc = (kc.float() * scale.view(-1, 1, 1)).to(torch.bfloat16)
+    out, _ = _run(q, kc, vc, idx, cu_q, cu_k, hq, hkv, d)
+    np.testing.assert_allclose(to_np64(out), _oracle(q, kc, vc, idx, cu_q, cu_k, d), **BF16_TOL)
