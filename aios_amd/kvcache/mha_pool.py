@@ -3,8 +3,9 @@
 Layout and API of python/aios/kvcache/mha_pool.py:8-68: one buffer
 ``[2, num_layers, num_pages, page_size=1, num_kv_heads, head_dim]`` (K = [0],
 V = [1]); layer ``i`` of K is the contiguous slice ``[num_pages, 1, Hkv, D]``.
-At 288 GB of HBM per MI355X the pool is sized by the caller (config 5 needs
-65,536 pages x 36 layers x 2 x 2 KiB = 9 GiB).
+At 288 GB of HBM per MI355X the pool is sized by the caller (the
+long-context workload, 36 layers of 8 kv-heads x 128 over 65,536 pages,
+needs 65,536 x 36 x 2 x 2 KiB = 9 GiB).
 """
 from __future__ import annotations
 

@@ -244,8 +244,8 @@ def _cpu_model_legs(seed: int, max_seconds: float) -> dict:
     from oracle.cpu_decoder import PagedCpuDecoder
 
     out = {}
-    for key, model, n_pre, ext, steps in (("c2_minimind_0p1b", "minimind-0.1b", 32, 0, 16),
-                                          ("c4_qwen3_0p6b", "qwen3-0.6b", 128, 2, 24)):
+    for key, model, n_pre, ext, steps in (("minimind_0p1b_model", "minimind-0.1b", 32, 0, 16),
+                                          ("qwen3_0p6b_model", "qwen3-0.6b", 128, 2, 24)):
         c = MODELS[model]
         w = init_weights(c, seed, "cpu")
         g = torch.Generator().manual_seed(seed + 3)
@@ -339,51 +339,53 @@ def cpu_baseline(host: "_HostLayers", op_host: "_HostLayers", seed: int, max_sec
     shape = host.shape
     scale = shape.num_layers / host.n
     legs = {}
-    c5 = {"layers_timed": host.n, "rows": shape.num_rows}
+    lc = {"layers_timed": host.n, "rows": shape.num_rows}
     for name, dtype in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
         med, cnt = _cpu_attention(host, dtype, max_seconds)
-        c5[f"{name}_us"] = round(med * scale * 1e6, 1)
-        c5[f"{name}_iterations"] = cnt
-    c5["gpu_us"] = gpu.get("step_us")
-    if c5["gpu_us"]:
-        c5["gpu_speedup_vs_bf16"] = round(c5["bf16_us"] / c5["gpu_us"], 1)
-        c5["gpu_speedup_vs_fp32"] = round(c5["fp32_us"] / c5["gpu_us"], 1)
-    c5["cpu_candidate_tokens_per_s_bf16"] = round(shape.num_rows / (c5["bf16_us"] * 1e-6), 2)
-    legs["c5_attention_step"] = c5
-    c1 = {"rows": op_host.shape.num_rows}
+        lc[f"{name}_us"] = round(med * scale * 1e6, 1)
+        lc[f"{name}_iterations"] = cnt
+    lc["gpu_us"] = gpu.get("step_us")
+    if lc["gpu_us"]:
+        lc["gpu_speedup_vs_bf16"] = round(lc["bf16_us"] / lc["gpu_us"], 1)
+        lc["gpu_speedup_vs_fp32"] = round(lc["fp32_us"] / lc["gpu_us"], 1)
+    lc["cpu_candidate_tokens_per_s_bf16"] = round(shape.num_rows / (lc["bf16_us"] * 1e-6), 2)
+    legs["long_context_attention_step"] = lc
+    ot = {"rows": op_host.shape.num_rows}
     for name, dtype in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
         med, cnt = _cpu_attention(op_host, dtype, max_seconds / 4, iters=200)
-        c1[f"{name}_us"] = round(med * 1e6, 1)
-    c1["gpu_us"] = gpu.get("op_test_us")
-    if c1["gpu_us"]:
-        c1["gpu_speedup_vs_bf16"] = round(c1["bf16_us"] / c1["gpu_us"], 1)
-    legs["c1_op_test_layer"] = c1
+        ot[f"{name}_us"] = round(med * 1e6, 1)
+    ot["gpu_us"] = gpu.get("op_test_us")
+    if ot["gpu_us"]:
+        ot["gpu_speedup_vs_bf16"] = round(ot["bf16_us"] / ot["gpu_us"], 1)
+    legs["op_test_layer"] = ot
     models = _cpu_model_legs(seed, max_seconds / 2)
-    for key, gkey in (("c2_minimind_0p1b", "c2_step_us"), ("c4_qwen3_0p6b", "c4_step_us")):
+    for key, gkey in (("minimind_0p1b_model", "minimind_0p1b_step_us"),
+                      ("qwen3_0p6b_model", "qwen3_0p6b_step_us")):
         leg = models[key]
         g_us = gpu.get(gkey)
         leg["gpu_decode_step_ms"] = None if g_us is None else round(g_us * 1e-3, 4)
         if g_us:
             leg["gpu_speedup_vs_bf16"] = round(leg["decode_step_bf16_ms"] / (g_us * 1e-3), 1)
         leg["cpu_candidate_tokens_per_s_bf16"] = round(leg["rows"] / (leg["decode_step_bf16_ms"] * 1e-3), 1)
-    ext_ms = gpu.get("c4_extension_ms")
-    models["c4_qwen3_0p6b"]["gpu_extension_prefill_ms"] = ext_ms
+    ext_ms = gpu.get("qwen3_0p6b_extension_ms")
+    models["qwen3_0p6b_model"]["gpu_extension_prefill_ms"] = ext_ms
     legs.update(models)
     return {
-        "value": c5["bf16_us"],
+        "value": lc["bf16_us"],
         "unit": "us/step",
         "cores": threads,
         "kind": "port",
         "sample": (f"{host.n} of {shape.num_layers} layers (distinct data) x {shape.num_rows} rows, "
                    f"bf16 torch CPU SDPA per row (oracle/sdpa_cpu.py), median of "
-                   f"{c5['bf16_iterations']} after 3 warmups, x{scale:g}"),
+                   f"{lc['bf16_iterations']} after 3 warmups, x{scale:g}"),
         "cpu_model": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
         "torch_threads": torch.get_num_threads(),
-        "gpu_figures": ("c5: graph-replayed decode step; c1: decode launches of the op test; "
-                        "c2/c4 decode step: GPU time per graph-replayed CandidateGroup step "
-                        "(model + sampling); c4 extension: GPU-event time of the eager 2-token "
-                        "prefill (launch gaps included)"),
+        "gpu_figures": ("long-context attention step: graph-replayed decode step; op test: "
+                        "decode launches of the op test; model legs' decode step: GPU time per "
+                        "graph-replayed CandidateGroup step (model + sampling); Qwen3-0.6B "
+                        "extension: GPU-event time of the eager 2-token prefill (launch gaps "
+                        "included)"),
         "legs": legs,
     }
 
@@ -704,9 +706,9 @@ CANDIDATE_LEGS = [
     ("candidate_group_attnres_0p214b",
      dict(model="minimind-attnres-0.214b", prefix_tokens=64, steps=32, runs=20, warmups=3,
           sampling=(0.35, 50, 0.9), min_new_tokens=2, max_candidates=24)),
-    # C3's refill leg: a greedy first round (top_k 1) forces refill rounds
-    # of 8 sampled branches (up to 24 candidates), each of 32 steps, with
-    # the round's suffix KV freed before the next round.
+    # The 0.214B Block-AttnRes refill leg: a greedy first round (top_k 1)
+    # forces refill rounds of 8 sampled branches (up to 24 candidates), each
+    # of 32 steps, with the round's suffix KV freed before the next round.
     ("candidate_group_attnres_0p214b_refill",
      dict(model="minimind-attnres-0.214b", prefix_tokens=64, steps=32, runs=10, warmups=2,
           sampling=(0.35, 1, 1.0), min_new_tokens=2, max_candidates=24)),
@@ -955,10 +957,10 @@ def main() -> int:
         from aios_amd.workloads import OP_TEST
 
         gpu = {"step_us": result["value"], "op_test_us": round(op_test_gpu(args.seed), 3)}
-        for key, name in (("c2_step_us", "candidate_group"),
-                          ("c4_step_us", "candidate_group_qwen3_0p6b")):
+        for key, name in (("minimind_0p1b_step_us", "candidate_group"),
+                          ("qwen3_0p6b_step_us", "candidate_group_qwen3_0p6b")):
             gpu[key] = result.get(name, {}).get("graph", {}).get("replayed_step_gpu_us")
-        gpu["c4_extension_ms"] = result.get("candidate_group_qwen3_0p6b", {}).get(
+        gpu["qwen3_0p6b_extension_ms"] = result.get("candidate_group_qwen3_0p6b", {}).get(
             "graph", {}).get("prefill_gpu_p50_ms")
         op_host = _HostLayers(make_decode_workload(OP_TEST, seed=args.seed, extra_token=True), 1)
         result["cpu_baseline"] = cpu_baseline(cpu_host, op_host, args.seed, args.cpu_seconds, gpu)

@@ -103,7 +103,8 @@ def test_multi_layer_isolation():
 
 
 def test_prefill_sized_append_long_context():
-    # 4096 tokens x 8 kv heads x 128 dims: one layer's prefill append at config 5.
+    # 4096 tokens x 8 kv heads x 128 dims: one layer's prefill append of the
+    # long-context (4096-token prefix) workload.
     t, hkv, d, pool = 4096, 8, 128, 65536
     g = torch.Generator().manual_seed(11)
     idx = torch.randperm(pool, generator=g)[:t].to(torch.int32)

@@ -666,7 +666,7 @@ def _record_rounds(eng):
 
 
 def test_attnres_0p214b_refill_rounds():
-    """C3's refill leg on the full 32-layer Block-AttnRes model: a greedy
+    """The refill leg of the 0.214B Block-AttnRes model (full 32 layers): a greedy
     first round (top_k 1) leaves one distinct candidate, so sampled refill
     rounds of 8 x 32 steps follow up to 24 candidates (ime.py:478-600).
     Every round starts with only the prefix pages held (the previous round's
