@@ -48,13 +48,19 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found: the gfx950 HIP backend cannot be built")
 
 
-# Per-source flags.  The decode combine compiled with LLVM's max-ILP machine
-# scheduler instead of the default occupancy-driven one: graph-replayed
-# long-context decode step 429.4-431.1 -> 422.8-423.6 us (three alternating
-# rounds on one box).  The decode main kernel (8.50 -> 8.61 us) and the
-# prefill measured slower with it and keep the default.
+# Per-source flags: LLVM's max-ILP machine scheduler instead of the default
+# occupancy-driven one for the short, latency-bound kernels.  The decode
+# combine: graph-replayed long-context decode step 429.4-431.1 -> 422.8-423.6
+# us (three alternating rounds on one box).  The model-side ops, depth mixer,
+# sampler, step preparation and KV append: every CandidateGroup leg's
+# replayed step 0.1-1.1% shorter (two rounds, both orders).  The decode main
+# kernel (8.50 -> 8.61 us) and the prefill measured slower with it and keep
+# the default.
+_MAX_ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
 SOURCE_FLAGS = {
-    "attn_combine.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    name: _MAX_ILP
+    for name in ("attn_combine.hip", "gemm_skinny.hip", "model_ops.hip", "attnres.hip",
+                 "sampling.hip", "cg_state.hip", "kv_append.hip")
 }
 
 
